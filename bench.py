@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Flash-attention forward benchmark on one MI355X (gfx950).
+
+One step = one flash-attention forward of the headline workload (BH=8 S=1024 d=64 causal, f16 in,
+f32 out) with Q/K/V already resident in HBM. Launches go through the C ABI (nc_flash_launch_async)
+on one stream; the timed region replays a HIP graph of back-to-back launches, bracketed by HIP
+events on that stream and a device synchronize on both sides, so the average per step is the
+kernel's average duration plus the (small) inter-kernel gap.
+
+Prints ONE JSON line (rank 0, N=1) with the metric of the benchmark plan, a `roofline` object for
+the flash kernel, and a `cpu_baseline` object: the CPU oracle (a port of the reference's scalar CPU
+reference) timed on this host on the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "not-cute-zig_amd"))
+
+import numpy as np  # noqa: E402
+
+import notcute_flash as nc  # noqa: E402
+from flash_workloads import CONFIGS, HEADLINE  # noqa: E402
+
+PEAK_F16_TFLOPS = 2516.6  # 256 CU x 4096 flop/clk x 2.4 GHz, dense
+PEAK_HBM_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "flash_fwd_{workload}_traffic.json")
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(wl, q, k, v, budget_s: float) -> dict:
+    """Time the CPU oracle (single thread) on the full workload, repeated until `budget_s` passes."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import flash_oracle  # noqa: E402  (checker / CPU baseline only)
+
+    o = np.zeros(wl.length("o"), dtype=np.float32)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        flash_oracle.flash_fwd(q, k, v, o, batch_heads=wl.batch_heads, seq_len=wl.seq_len, head_dim=wl.head_dim,
+                               q_stride=wl.stride("q"), k_stride=wl.stride("k"), v_stride=wl.stride("v"),
+                               o_stride=wl.stride("o"), scale=wl.scale, causal=wl.causal, threads=1)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    flops = wl.work()["flops"]
+    return {
+        "value": flops * reps / el / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"full {wl.name} workload ({wl.describe()}) x {reps} repetitions, {el:.1f} s, one thread, "
+                  f"C restatement of src/main.zig:1271-1307 (-O3, no fast-math)",
+    }, o
+
+
+def calibrate_copy(mod: nc.Module, stream: nc.Stream, nbytes: int, iters: int) -> None:
+    """Launch the plain copy kernel on a known byte count (for rocprofv3 counter calibration)."""
+    n16 = nbytes // 16
+    src = nc.DeviceBuffer(n16 * 16)
+    dst = nc.DeviceBuffer(n16 * 16)
+    src.memset(1)
+    fn = mod.get_function("nc_util_copy_b128")
+    import ctypes
+
+    ps = [ctypes.c_void_p(src.ptr), ctypes.c_void_p(dst.ptr), ctypes.c_uint64(n16)]
+    for _ in range(iters):
+        fn.launch((1024,), (256,), ps, stream=stream.handle)
+    stream.synchronize()
+    src.free()
+    dst.free()
+    log(f"calibration copy: {iters} x {n16 * 16} bytes read + written")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000, help="timed steps (flash launches)")
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(CONFIGS))
+    ap.add_argument("--graph-batch", type=int, default=100, help="launches captured per HIP graph")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget (0: skip)")
+    ap.add_argument("--ref-iters", type=int, default=20, help="iterations of the per-launch event timing")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run the plain copy kernel on MIB MiB (profiling runs only)")
+    ap.add_argument("--no-verify", action="store_true", help="skip the oracle check of the output")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              f"(the path shards by (batch, head) slices with no exchange; see the design notes)", file=sys.stderr)
+        return 2
+    for var in ("RANK", "WORLD_SIZE"):
+        if int(os.environ.get(var, "0") or 0) > (0 if var == "RANK" else 1):
+            print("bench.py: multi-rank launch is not supported by this one-GPU build", file=sys.stderr)
+            return 2
+
+    wl = CONFIGS[args.workload]
+    opts = wl.options()
+    work = wl.work()
+    sel = nc.select_kernel(opts)
+    log(f"bench: {wl.describe()} -> {sel.name.decode()} grid={sel.grid[0]} threads={sel.threads}")
+
+    nc.init()
+    mod = nc.Module.load_embedded()
+    q, k, v = wl.make_inputs()
+    dq, dk, dv = (nc.DeviceBuffer.from_array(x) for x in (q, k, v))
+    do = nc.DeviceBuffer(wl.length("o") * 4)
+    do.memset(0)
+    stream = nc.Stream()
+
+    def launch():
+        nc.flash_launch(mod, dq, dk, dv, do, opts, stream=stream.handle)
+
+    # correctness of what is timed
+    launch()
+    stream.synchronize()
+    max_abs = None
+    if not args.no_verify:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import flashcheck  # noqa: E402  (checker only)
+
+        ref = flashcheck.oracle(wl, q, k, v, rows=None if wl.seq_len <= 1024 else np.arange(0, wl.seq_len, 97))
+        idx = flashcheck.active_index(wl, None if wl.seq_len <= 1024 else np.arange(0, wl.seq_len, 97))
+        out = do.download(np.float32, wl.length("o"))
+        max_abs, max_rel = flashcheck.errors(out, ref, idx)
+        log(f"bench: parity vs oracle max-abs {max_abs:.3e} max-rel {max_rel:.3e}")
+        if not (max_abs <= flashcheck.MAX_ABS and max_rel <= flashcheck.MAX_REL):
+            print(json.dumps({"error": "parity failure", "max_abs": max_abs, "max_rel": max_rel}))
+            return 1
+
+    # warmup (eager)
+    for _ in range(args.warmup):
+        launch()
+    stream.synchronize()
+
+    # reference semantics (src/benchmark.zig:35-92): one event pair per launch, mean/min/max
+    fn = mod.get_function(sel.name.decode())
+    ka = nc.pack_args(opts, sel, dq.ptr, dk.ptr, dv.ptr, do.ptr)
+    per_launch = nc.run_kernel(fn, tuple(sel.grid), (sel.threads,), [ka], warmup=5, iters=args.ref_iters,
+                               bytes_=work["bytes"], flops=work["flops_reference"], stream=stream.handle)
+
+    # timed region: graphs of back-to-back launches
+    gb = max(1, min(args.graph_batch, args.steps))
+    reps = max(1, args.steps // gb)
+    steps = gb * reps
+    graph = nc.Graph.capture(stream, lambda: [launch() for _ in range(gb)])
+    graph.launch(stream)
+    stream.synchronize()
+    ev0, ev1 = nc.Event(), nc.Event()
+    nc.synchronize()
+    ev0.record(stream.handle)
+    for _ in range(reps):
+        graph.launch(stream)
+    ev1.record(stream.handle)
+    ev1.synchronize()
+    nc.synchronize()
+    total_ms = nc.Event.elapsed(ev0, ev1)
+    ms = total_ms / steps
+    graph.destroy()
+    log(f"bench: {steps} steps in {total_ms:.3f} ms -> {ms * 1e3:.3f} us/step; per-launch event timing "
+        f"mean {per_launch.mean_ms * 1e3:.2f} us min {per_launch.min_ms * 1e3:.2f} us")
+
+    if args.calibrate_copy:
+        calibrate_copy(mod, stream, args.calibrate_copy << 20, 10)
+
+    tflops = work["flops"] / (ms * 1e-3) / 1e12
+    ai = work["flops"] / work["bytes"]
+    roof_tflops = min(PEAK_F16_TFLOPS, ai * PEAK_HBM_GBPS / 1e3)
+    bound = "hbm" if ai * PEAK_HBM_GBPS / 1e3 < PEAK_F16_TFLOPS else "mfma"
+    traffic = None
+    tf = TRAFFIC_FILE.format(workload=wl.name)
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
+    if bound == "hbm":
+        achieved = work["bytes"] / (ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / PEAK_HBM_GBPS, 5), "traffic": traffic}
+    else:
+        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tflops / PEAK_F16_TFLOPS, 5), "traffic": traffic}
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu, _ = cpu_baseline(wl, q, k, v, args.cpu_seconds)
+        log(f"bench: cpu baseline {cpu['value'] * 1e3:.3f} GFLOP/s ({cpu['sample']})")
+
+    rec = {
+        "metric": "flash-attn fwd TFLOP/s + % f16 MFMA peak, BH=8 S=1024 d=64 causal",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"{wl.name}: flash-attn fwd BH={wl.batch_heads} S={wl.seq_len} d={wl.head_dim} "
+                               f"{'causal' if wl.causal else 'non-causal'}, Q/K/V f16 N(0,1) seed {wl.seed}, "
+                               f"scale {wl.scale:g}, f32 accumulate/out",
+                   "batch_heads": wl.batch_heads, "seq_len": wl.seq_len, "head_dim": wl.head_dim,
+                   "causal": wl.causal, "kernel": sel.name.decode(), "parallelism": "single-gpu"},
+        "pct_f16_mfma_peak": round(100.0 * tflops / PEAK_F16_TFLOPS, 3),
+        "pct_roofline": round(100.0 * tflops / roof_tflops, 3),
+        "flops_per_step": work["flops"],
+        "flops_per_step_reference_formula": work["flops_reference"],
+        "bytes_per_step": work["bytes"],
+        "timing": "HIP events around graph replays of back-to-back launches on the launch stream",
+        "per_launch_event_ms": {"mean": per_launch.mean_ms, "min": per_launch.min_ms, "max": per_launch.max_ms,
+                                "iters": args.ref_iters},
+        "parity_max_abs": max_abs,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+    for b in (dq, dk, dv, do):
+        b.free()
+    stream.destroy()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,279 @@
+// flash.cpp — flash-attention host API (the role of src/flash.zig in the reference).
+//
+//   nc_flash_options_init / nc_flash_validate   <- flash.Options + validate   (src/flash.zig:5-29)
+//   nc_flash_select_kernel[_for]                 <- KernelSelection + selectKernel (src/flash.zig:72-96)
+//   nc_flash_launch[_async]                      <- launch + requireLen       (src/flash.zig:31-70, 98-100)
+//
+// Validation keeps the reference's rules and error (InvalidValue); the optional row strides extend
+// them so that a padded row pitch can be described (a layout the reference API cannot express).
+// Dispatch keeps the reference's output contract (a kernel name, a label and a thread count) and
+// adds the launch geometry, because the gfx950 kernels tile queries in 32/64/128-row blocks rather
+// than the fixed 16 of src/config.zig:19 that the reference's callers hard-code.
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <limits>
+
+#include "notcute_flash.h"
+
+namespace {
+
+// Geometry of one nc_flash_fwd_* kernel; must agree with Cfg<> in flash_fwd.hip.
+struct Geometry {
+    uint32_t nq, ns;  // query waves, key-split waves
+    uint32_t bm() const { return 32 * nq; }
+    uint32_t bn() const { return 32 * ns; }
+    uint32_t threads() const { return 64 * nq * ns; }
+    uint32_t lds_bytes(uint32_t d) const {
+        const uint32_t nw = nq * ns;
+        const uint32_t dv = d < 32 ? 32 : d;
+        const uint32_t k_bytes = bn() * (d + 8) * 2;
+        const uint32_t v_bytes = dv * (bn() + 8) * 2;
+        const uint32_t o_bytes = nw * 32 * (d + 4) * 4;
+        const uint32_t stage = k_bytes + v_bytes;
+        return (stage > o_bytes ? stage : o_bytes) + nw * 32 * 2 * 4;
+    }
+};
+
+struct Variant {
+    const char *name;
+    uint32_t d;
+    uint32_t bm;
+    bool causal;
+    bool aligned;
+};
+
+const Variant kVariants[] = {
+    {"nc_flash_fwd_d16_m128_full", 16, 128, false, true},
+    {"nc_flash_fwd_d16_m128_causal", 16, 128, true, true},
+    {"nc_flash_fwd_d16_m64_full", 16, 64, false, true},
+    {"nc_flash_fwd_d16_m64_causal", 16, 64, true, true},
+    {"nc_flash_fwd_d16_m32_full", 16, 32, false, true},
+    {"nc_flash_fwd_d16_m32_causal", 16, 32, true, true},
+    {"nc_flash_fwd_d32_m128_full", 32, 128, false, true},
+    {"nc_flash_fwd_d32_m128_causal", 32, 128, true, true},
+    {"nc_flash_fwd_d32_m64_full", 32, 64, false, true},
+    {"nc_flash_fwd_d32_m64_causal", 32, 64, true, true},
+    {"nc_flash_fwd_d32_m32_full", 32, 32, false, true},
+    {"nc_flash_fwd_d32_m32_causal", 32, 32, true, true},
+    {"nc_flash_fwd_d64_m128_full", 64, 128, false, true},
+    {"nc_flash_fwd_d64_m128_causal", 64, 128, true, true},
+    {"nc_flash_fwd_d64_m64_full", 64, 64, false, true},
+    {"nc_flash_fwd_d64_m64_causal", 64, 64, true, true},
+    {"nc_flash_fwd_d64_m32_full", 64, 32, false, true},
+    {"nc_flash_fwd_d64_m32_causal", 64, 32, true, true},
+    {"nc_flash_fwd_d16_m64_full_unaligned", 16, 64, false, false},
+    {"nc_flash_fwd_d16_m64_causal_unaligned", 16, 64, true, false},
+    {"nc_flash_fwd_d32_m64_full_unaligned", 32, 64, false, false},
+    {"nc_flash_fwd_d32_m64_causal_unaligned", 32, 64, true, false},
+    {"nc_flash_fwd_d64_m64_full_unaligned", 64, 64, false, false},
+    {"nc_flash_fwd_d64_m64_causal_unaligned", 64, 64, true, false},
+};
+
+Geometry geometry_for(uint32_t bm) {
+    switch (bm) {
+    case 128: return {4, 1};
+    case 64: return {2, 2};
+    default: return {1, 4};
+    }
+}
+
+const Variant *find_variant(uint32_t d, uint32_t bm, bool causal, bool aligned) {
+    for (const auto &v : kVariants)
+        if (v.d == d && v.bm == bm && v.causal == causal && v.aligned == aligned) return &v;
+    return nullptr;
+}
+
+uint64_t row_stride_of(uint64_t rs, uint64_t d) { return rs == 0 ? d : rs; }
+
+bool mul_overflows(uint64_t a, uint64_t b, uint64_t *out) {
+    if (a != 0 && b > std::numeric_limits<uint64_t>::max() / a) return true;
+    *out = a * b;
+    return false;
+}
+
+// The reference's selectKernel, restated (src/flash.zig:78-96), so every selection records which
+// reference kernel it stands in for.
+const char *reference_kernel(const nc_flash_options &o) {
+    if (o.head_dim <= 32 && o.seq_len <= 256 && o.batch_heads <= 8) return "flash_attention_fwd_v2";
+    if (o.head_dim == 64 && !o.causal && o.seq_len <= 256 && o.batch_heads <= 8) return "flash_attention_fwd_v2";
+    if (o.head_dim == 64 && o.seq_len >= 512) return "flash_attention_fwd_h64_bn32";
+    if (o.head_dim == 64) return "flash_attention_fwd_h64";
+    return "flash_attention_fwd_opt";
+}
+
+// MI355X block-size choice: prefer the 128-query block (4 waves share every staged K/V tile)
+// while the grid still gives every one of the 256 CUs two workgroups; otherwise shrink the query
+// block and split each block's keys over more waves, so short sequences still fill the chip.
+uint32_t choose_block_m(const nc_flash_options &o) {
+    constexpr uint64_t kCUs = 256;
+    auto wgs = [&](uint64_t bm) { return ((o.seq_len + bm - 1) / bm) * o.batch_heads; };
+    if (wgs(128) >= 2 * kCUs) return 128;
+    if (wgs(64) >= kCUs) return 64;
+    return 32;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selection *out) {
+    if (!out) return NC_ERROR_INVALID_VALUE;
+    int st = nc_flash_validate(opts);
+    if (st) return st;
+    const nc_flash_options &o = *opts;
+    const uint64_t d = o.head_dim;
+    // 16-byte vector path: every Q/K/V row start is 16-byte aligned and O rows are float4 aligned.
+    const bool strides_ok = o.q_stride % 8 == 0 && o.k_stride % 8 == 0 && o.v_stride % 8 == 0 &&
+                            o.o_stride % 4 == 0 && row_stride_of(o.q_row_stride, d) % 8 == 0 &&
+                            row_stride_of(o.k_row_stride, d) % 8 == 0 &&
+                            row_stride_of(o.v_row_stride, d) % 8 == 0 &&
+                            row_stride_of(o.o_row_stride, d) % 4 == 0;
+    const bool aligned = vec_ok && strides_ok;
+    const uint32_t bm = aligned ? choose_block_m(o) : 64;
+    const Variant *v = find_variant((uint32_t)d, bm, o.causal != 0, aligned);
+    if (!v) return NC_ERROR_NOT_FOUND;
+    const Geometry g = geometry_for(bm);
+    const uint64_t nqb = (o.seq_len + bm - 1) / bm;
+    uint64_t grid = 0;
+    if (mul_overflows(nqb, o.batch_heads, &grid) || grid > 0xffffffffull) return NC_ERROR_OVERFLOW;
+    std::memset(out, 0, sizeof *out);
+    out->name = v->name;
+    out->label = v->name;
+    out->reference_name = reference_kernel(o);
+    out->threads = g.threads();
+    out->grid[0] = (uint32_t)grid;
+    out->grid[1] = 1;
+    out->grid[2] = 1;
+    out->block_m = g.bm();
+    out->block_n = g.bn();
+    out->kv_splits = g.ns;
+    out->lds_bytes = g.lds_bytes((uint32_t)d);
+    out->aligned = aligned ? 1u : 0u;
+    return NC_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+void nc_flash_options_init(nc_flash_options *opts) {
+    if (!opts) return;
+    std::memset(opts, 0, sizeof *opts);
+    opts->batch_heads = 1;  // src/flash.zig:6
+    opts->causal = 0;       // src/flash.zig:14
+}
+
+int nc_flash_validate(const nc_flash_options *opts) {
+    if (!opts) return NC_ERROR_INVALID_VALUE;
+    const nc_flash_options &o = *opts;
+    if (o.batch_heads == 0 || o.seq_len == 0) return NC_ERROR_INVALID_VALUE;                   // :17
+    if (o.head_dim != 16 && o.head_dim != 32 && o.head_dim != 64) return NC_ERROR_INVALID_VALUE; // :18
+    const uint64_t d = o.head_dim;
+    const uint64_t rows[4] = {row_stride_of(o.q_row_stride, d), row_stride_of(o.k_row_stride, d),
+                              row_stride_of(o.v_row_stride, d), row_stride_of(o.o_row_stride, d)};
+    const uint64_t slices[4] = {o.q_stride, o.k_stride, o.v_stride, o.o_stride};
+    for (int i = 0; i < 4; ++i) {
+        if (rows[i] < d) return NC_ERROR_INVALID_VALUE;
+        // Smallest slice that holds seq_len rows: (S-1)*row + d; with row == d this is the
+        // reference's S*d (src/flash.zig:20-27).
+        uint64_t span = 0;
+        if (mul_overflows(o.seq_len - 1, rows[i], &span) || span > std::numeric_limits<uint64_t>::max() - d)
+            return NC_ERROR_OVERFLOW;
+        if (slices[i] < span + d) return NC_ERROR_INVALID_VALUE;
+        uint64_t total = 0;
+        if (mul_overflows(o.batch_heads, slices[i], &total)) return NC_ERROR_OVERFLOW;
+    }
+    // The kernels index rows and keys with 32-bit integers.
+    if (o.seq_len > (uint64_t)std::numeric_limits<int32_t>::max() - 256) return NC_ERROR_INVALID_VALUE;
+    if (o.batch_heads > 0xffffffffull) return NC_ERROR_INVALID_VALUE;
+    return NC_SUCCESS;
+}
+
+int nc_flash_select_kernel(const nc_flash_options *opts, nc_flash_kernel_selection *out) {
+    return select_impl(opts, true, out);
+}
+
+int nc_flash_select_kernel_for(const nc_flash_options *opts, const void *q, const void *k, const void *v,
+                               const void *o, nc_flash_kernel_selection *out) {
+    return select_impl(opts, aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o), out);
+}
+
+int nc_flash_pack_args(const nc_flash_options *opts, const nc_flash_kernel_selection *sel, const uint16_t *q,
+                       const uint16_t *k, const uint16_t *v, float *o, nc_flash_kernel_args *out) {
+    if (!opts || !sel || !out || sel->block_m == 0) return NC_ERROR_INVALID_VALUE;
+    const nc_flash_options &op = *opts;
+    std::memset(out, 0, sizeof *out);
+    out->q = q;
+    out->k = k;
+    out->v = v;
+    out->o = o;
+    out->seq_len = op.seq_len;
+    out->head_dim = op.head_dim;
+    out->q_stride = op.q_stride;
+    out->k_stride = op.k_stride;
+    out->v_stride = op.v_stride;
+    out->o_stride = op.o_stride;
+    out->scale = op.scale;
+    out->causal = op.causal ? 1u : 0u;
+    out->q_row_stride = row_stride_of(op.q_row_stride, op.head_dim);
+    out->k_row_stride = row_stride_of(op.k_row_stride, op.head_dim);
+    out->v_row_stride = row_stride_of(op.v_row_stride, op.head_dim);
+    out->o_row_stride = row_stride_of(op.o_row_stride, op.head_dim);
+    out->batch_heads = (uint32_t)op.batch_heads;
+    out->num_q_blocks = (uint32_t)((op.seq_len + sel->block_m - 1) / sel->block_m);
+    return NC_SUCCESS;
+}
+
+int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
+                          const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts,
+                          nc_stream stream) {
+    int st = nc_flash_validate(opts);  // src/flash.zig:39
+    if (st) return st;
+    if (!module || !q || !k || !v || !o) return NC_ERROR_INVALID_VALUE;
+    // requireLen (src/flash.zig:40-43, 98-100): each buffer holds batch_heads full slices.
+    const uint64_t need[4] = {opts->batch_heads * opts->q_stride, opts->batch_heads * opts->k_stride,
+                              opts->batch_heads * opts->v_stride, opts->batch_heads * opts->o_stride};
+    const uint64_t have[4] = {q_len, k_len, v_len, o_len};
+    for (int i = 0; i < 4; ++i)
+        if (have[i] < need[i]) return NC_ERROR_INVALID_VALUE;
+
+    nc_flash_kernel_selection sel;
+    st = nc_flash_select_kernel_for(opts, q, k, v, o, &sel);
+    if (st) return st;
+    nc_function fn = nullptr;
+    st = nc_module_get_function(&fn, module, sel.name);
+    if (st) return st;
+    nc_flash_kernel_args args;
+    st = nc_flash_pack_args(opts, &sel, q, k, v, o, &args);
+    if (st) return st;
+    nc_launch_config cfg;
+    std::memset(&cfg, 0, sizeof cfg);
+    cfg.grid[0] = sel.grid[0];
+    cfg.grid[1] = sel.grid[1];
+    cfg.grid[2] = sel.grid[2];
+    cfg.block[0] = sel.threads;
+    cfg.block[1] = 1;
+    cfg.block[2] = 1;
+    cfg.shared_mem_bytes = 0;
+    cfg.stream = stream;
+    void *params[] = {&args};
+    return nc_function_launch(fn, &cfg, params);
+}
+
+int nc_flash_launch(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
+                    const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts) {
+    return nc_flash_launch_async(module, q, q_len, k, k_len, v, v_len, o, o_len, opts, nullptr);
+}
+
+int nc_flash_work_model(const nc_flash_options *opts, nc_flash_work *out) {
+    if (!opts || !out) return NC_ERROR_INVALID_VALUE;
+    const uint64_t bh = opts->batch_heads, s = opts->seq_len, d = opts->head_dim;
+    const uint64_t eff = opts->causal ? (s * (s + 1)) / 2 : s * s;  // src/main.zig:1032
+    out->flops_reference = bh * (4 * eff * d);                      // src/main.zig:1033
+    out->flops_halfsquare = (4 * bh * s * s * d) / (opts->causal ? 2 : 1);
+    out->bytes = bh * s * d * (2 * 3 + 4);                          // src/main.zig:1034
+    return NC_SUCCESS;
+}
+
+}  // extern "C"

@@ -1,0 +1,398 @@
+// flash_fwd.hip — flash-attention forward for MI355X (gfx950, CDNA4, wave64).
+//
+// Replaces the reference's device kernels flash_attention_fwd_{v2,opt,h64,h64_bn32,h64_causal} and
+// the legacy flash_attention_fwd (src/flash_v2.zig:23, src/flash_opt.zig:17, src/flash_h64.zig:21,
+// src/flash_h64_bn32.zig:26, src/flash_h64_causal.zig:20, src/kernels.zig:380). Same math:
+// O = softmax(scale * Q K^T, causal mask) V per (batch, head) slice, f16 inputs, f32 accumulation,
+// f32 output, online softmax over key tiles with the row max/sum rescale of
+// src/flash_h64_bn32.zig:139-211, P rounded to f16 for the PV product while the row sum uses the
+// unrounded weights (src/flash_h64_bn32.zig:180-185), final O / l (src/flash_h64_bn32.zig:246-260).
+//
+// gfx950 formulation
+//   * One wave owns 32 queries. It computes the transposed score tile S^T = K * Q^T with
+//     v_mfma_f32_32x32x16_f16 (A = K rows from LDS, B = Q^T held in VGPRs for the whole sweep).
+//     In the 32x32 accumulator layout lane l holds column (query) l%32 and 16 rows (keys)
+//     8*(r/4) + 4*(l/32) + r%4, so the softmax row statistics of a query live in one lane pair
+//     (l, l^32): max and sum are 15 in-lane ops plus one v_permlane32_swap.
+//   * The exponentiated tile P^T is already in the B-operand layout of the PV product
+//     O^T += V^T * P^T (registers 0..7 -> keys 0..15, 8..15 -> keys 16..31), so P never touches LDS.
+//     V^T is staged transposed in LDS with keys permuted to match (bits 2 and 3 of the key index
+//     within each 16-key group swapped), which turns every A-operand fetch into one ds_read_b128.
+//   * A workgroup has NQ x NS waves: NQ query groups of 32 rows, each of whose key range is split
+//     over NS waves (key sub-tile j of every BN = 32*NS staged keys goes to wave j). NS > 1 fills
+//     the chip on short sequences; the NS partial (m, l, O) triples are merged through LDS with the
+//     same rescale rule. All variants share the LDS epilogue, which also coalesces the f32 stores.
+//   * Causal: key sub-tiles entirely above the diagonal are skipped per wave, and key blocks past
+//     the workgroup's last query are never staged. Heavy (late) query blocks are dispatched first and
+//     workgroups of the same heads are kept on one XCD so their K/V stay in that XCD's L2.
+//   * exp is v_exp_f32 on log2-scaled scores (scale * log2(e) folded into one multiply).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "notcute_flash.h"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+
+// max / sum of x over the lane pair (l, l^32); both lanes get the identical result.
+__device__ __forceinline__ float pair_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Position of key kk (block-relative) inside a staged V^T row: swap bits 2 and 3.
+__device__ __forceinline__ int vt_pos(int kk) {
+    return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
+}
+
+// 8 consecutive f16 values (16 bytes). VEC: one 16-byte load (caller guarantees alignment).
+template <bool VEC>
+__device__ __forceinline__ u32x4 load8(const uint16_t *p) {
+    if constexpr (VEC) {
+        return *reinterpret_cast<const u32x4 *>(p);
+    } else {
+        u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = uint32_t(p[2 * i]) | (uint32_t(p[2 * i + 1]) << 16);
+        return r;
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store4(float *p, floatx4 v) {
+    if constexpr (VEC) {
+        *reinterpret_cast<floatx4 *>(p) = v;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = v[i];
+    }
+}
+
+template <int D, int NQ, int NS>
+struct Cfg {
+    static constexpr int NW = NQ * NS;           // waves per workgroup
+    static constexpr int NT = NW * 64;           // threads per workgroup
+    static constexpr int BM = 32 * NQ;           // query rows per workgroup
+    static constexpr int BN = 32 * NS;           // keys staged per iteration
+    static constexpr int DV = D < 32 ? 32 : D;   // V^T rows in LDS (head 16 padded with zero rows)
+    static constexpr int MT = DV / 32;           // 32-row output tiles per wave
+    static constexpr int KP = D + 8;             // K row pitch in LDS, halves (16 B pad: no bank clash)
+    static constexpr int VP = BN + 8;            // V^T row pitch in LDS, halves
+    static constexpr int K_BYTES = BN * KP * 2;
+    static constexpr int V_BYTES = DV * VP * 2;
+    static constexpr int OP = D + 4;             // merge-buffer row pitch, floats
+    static constexpr int O_BYTES = NW * 32 * OP * 4;
+    static constexpr int STAGE_BYTES = K_BYTES + V_BYTES;
+    static constexpr int ML_OFF = STAGE_BYTES > O_BYTES ? STAGE_BYTES : O_BYTES;
+    static constexpr int LDS_BYTES = ML_OFF + NW * 32 * 2 * 4;
+    static constexpr int KU = BN * (D / 8);         // 16-byte K chunks per staged block
+    static constexpr int VU = (BN / 4) * (D / 8);   // V units of 4 keys x 8 columns
+    static constexpr int KREG = (KU + NT - 1) / NT;
+    static constexpr int VREG = (VU + NT - 1) / NT;
+};
+
+template <int D, int NQ, int NS, bool CAUSAL, bool VEC>
+__device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
+    using C = Cfg<D, NQ, NS>;
+    __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+
+    if (a.head_dim != (uint64_t)D || a.seq_len == 0) return;  // as src/flash_h64_bn32.zig:40
+
+    const int S = (int)a.seq_len;
+    const uint32_t bh = a.batch_heads;
+    const uint32_t nqb = a.num_q_blocks;
+
+    // Workgroup -> (head, query block). Consecutive workgroup ids go round-robin to the 8 XCDs;
+    // give each XCD a contiguous range of heads and hand out late (heavier, under a causal mask)
+    // query blocks first.
+    const uint32_t L = blockIdx.x;
+    uint32_t head, qb_rev;
+    if ((bh & 7u) == 0) {
+        const uint32_t hpx = bh >> 3, x = L & 7u, idx = L >> 3;
+        head = x * hpx + idx % hpx;
+        qb_rev = idx / hpx;
+    } else {
+        head = L % bh;
+        qb_rev = L / bh;
+    }
+    const int qb = (int)(nqb - 1u - qb_rev);
+
+    const int tid = threadIdx.x;
+    const int w = tid >> 6;
+    const int lane = tid & 63;
+    const int c = lane & 31;
+    const int hh = lane >> 5;
+    const int qg = w / NS;
+    const int s = w % NS;
+
+    const int q0 = qb * C::BM;        // first query of the workgroup
+    const int qw0 = q0 + 32 * qg;     // first query of this wave
+    const int qrow = qw0 + c;         // this lane's query
+    const int qw_last = min(qw0 + 31, S - 1);
+
+    const uint16_t *qbase = a.q + (size_t)head * a.q_stride;
+    const uint16_t *kbase = a.k + (size_t)head * a.k_stride;
+    const uint16_t *vbase = a.v + (size_t)head * a.v_stride;
+    float *obase = a.o + (size_t)head * a.o_stride;
+    const size_t qrs = a.q_row_stride, krs = a.k_row_stride, vrs = a.v_row_stride, ors = a.o_row_stride;
+
+    uint16_t *klds = reinterpret_cast<uint16_t *>(smem);
+    uint16_t *vlds = reinterpret_cast<uint16_t *>(smem + C::K_BYTES);
+
+    // Q^T B-operand, resident for the whole key sweep: lane (c, hh) holds Q[qrow][16kk + 8hh .. +7].
+    half8 qf[D / 16];
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+        u32x4 t = {0u, 0u, 0u, 0u};
+        if (qrow < S) t = load8<VEC>(qbase + (size_t)qrow * qrs + 16 * kk + 8 * hh);
+        qf[kk] = __builtin_bit_cast(half8, t);
+    }
+
+    if constexpr (D < 32) {  // zero V^T rows D..31 once; staging never writes them
+        for (int i = tid; i < (32 - D) * C::VP / 2; i += C::NT)
+            reinterpret_cast<uint32_t *>(vlds + D * C::VP)[i] = 0u;
+    }
+
+    const int kv_end = CAUSAL ? min(S, q0 + C::BM) : S;
+    const int nblk = (kv_end + C::BN - 1) / C::BN;
+
+    u32x4 kreg[C::KREG];
+    u32x4 vreg[C::VREG][4];
+
+    auto load_block = [&](int blk) {
+        const int kb0 = blk * C::BN;
+#pragma unroll
+        for (int i = 0; i < C::KREG; ++i) {
+            const int u = tid + i * C::NT;
+            if (C::KU % C::NT == 0 || u < C::KU) {
+                const int key = u / (D / 8), ch = u % (D / 8);
+                const int kr = kb0 + key;
+                u32x4 t = {0u, 0u, 0u, 0u};
+                if (kr < S) t = load8<VEC>(kbase + (size_t)kr * krs + 8 * ch);
+                kreg[i] = t;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::VREG; ++i) {
+            const int u = tid + i * C::NT;
+            if (C::VU % C::NT == 0 || u < C::VU) {
+                const int kq = u / (D / 8), ch = u % (D / 8);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int kr = kb0 + 4 * kq + j;
+                    u32x4 t = {0u, 0u, 0u, 0u};
+                    if (kr < S) t = load8<VEC>(vbase + (size_t)kr * vrs + 8 * ch);
+                    vreg[i][j] = t;
+                }
+            }
+        }
+    };
+
+    auto store_block = [&]() {
+#pragma unroll
+        for (int i = 0; i < C::KREG; ++i) {
+            const int u = tid + i * C::NT;
+            if (C::KU % C::NT == 0 || u < C::KU) {
+                const int key = u / (D / 8), ch = u % (D / 8);
+                *reinterpret_cast<u32x4 *>(klds + key * C::KP + 8 * ch) = kreg[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::VREG; ++i) {
+            const int u = tid + i * C::NT;
+            if (C::VU % C::NT == 0 || u < C::VU) {
+                const int kq = u / (D / 8), ch = u % (D / 8);
+                const int pos = vt_pos(4 * kq);
+#pragma unroll
+                for (int cp = 0; cp < 4; ++cp) {  // column pair (2cp, 2cp+1) of the 8 staged columns
+                    const uint32_t w0 = vreg[i][0][cp], w1 = vreg[i][1][cp];
+                    const uint32_t w2 = vreg[i][2][cp], w3 = vreg[i][3][cp];
+                    u32x2 even = {(w0 & 0xffffu) | (w1 << 16), (w2 & 0xffffu) | (w3 << 16)};
+                    u32x2 odd = {(w0 >> 16) | (w1 & 0xffff0000u), (w2 >> 16) | (w3 & 0xffff0000u)};
+                    *reinterpret_cast<u32x2 *>(vlds + (8 * ch + 2 * cp) * C::VP + pos) = even;
+                    *reinterpret_cast<u32x2 *>(vlds + (8 * ch + 2 * cp + 1) * C::VP + pos) = odd;
+                }
+            }
+        }
+    };
+
+    const float sc = a.scale * kLog2e;
+    float m = neg_inf();  // running max of log2-scaled scores (same in both lanes of a pair)
+    float l = 0.f;        // this lane's partial row sum
+    floatx16 o[C::MT];
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt) o[mt] = floatx16{};
+
+    if (nblk > 0) load_block(0);
+    for (int blk = 0; blk < nblk; ++blk) {
+        if (blk > 0) __syncthreads();  // every wave is done reading the previous block
+        store_block();
+        __syncthreads();
+        if (blk + 1 < nblk) load_block(blk + 1);  // in flight while this block is computed
+
+        const int kt0 = blk * C::BN + 32 * s;  // this wave's key sub-tile
+        bool run = kt0 < S;
+        if (CAUSAL) run = run && kt0 <= qw_last;
+        if (!run) continue;
+
+        // S^T = K * Q^T over the head dimension.
+        floatx16 acc = floatx16{};
+        const uint16_t *krow = klds + (32 * s + c) * C::KP + 8 * hh;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+            const half8 kf = *reinterpret_cast<const half8 *>(krow + 16 * kk);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], acc, 0, 0, 0);
+        }
+
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = acc[r] * sc;
+        const bool need_mask = (kt0 + 32 > S) || (CAUSAL && kt0 + 31 > qw0);
+        if (need_mask) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kt0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                const bool masked = key >= S || (CAUSAL && key > qrow);
+                if (masked) p[r] = neg_inf();
+            }
+        }
+
+        float tmax = p[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, p[r]);
+        tmax = pair_max(tmax);
+        const float m_new = fmaxf(m, tmax);
+        const float m_use = (m_new == neg_inf()) ? 0.f : m_new;  // fully masked so far: weights 0
+        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+        float psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = __builtin_amdgcn_exp2f(p[r] - m_use);
+            psum += p[r];
+        }
+        l = l * alpha + psum;
+        m = m_new;
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt) o[mt] *= alpha;
+
+        half8 pf[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pf[ks][j] = (_Float16)p[8 * ks + j];
+
+        // O^T += V^T * P^T.
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt) {
+            const uint16_t *vrow = vlds + (32 * mt + c) * C::VP + 32 * s + 8 * hh;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const half8 vf = *reinterpret_cast<const half8 *>(vrow + 16 * ks);
+                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], o[mt], 0, 0, 0);
+            }
+        }
+    }
+
+    // Epilogue: per-wave (m, l, O^T) into LDS, merge the NS key splits, normalise, store O rows.
+    __syncthreads();
+    float *ob = reinterpret_cast<float *>(smem);
+    float *mb = reinterpret_cast<float *>(smem + C::ML_OFF);
+    float *lb = mb + C::NW * 32;
+    const float lt = pair_sum(l);
+    {
+        float *dst = ob + (w * 32 + c) * C::OP;
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 32 * mt + 8 * i + 4 * hh;
+                if (d < D) {
+                    floatx4 t = {o[mt][4 * i], o[mt][4 * i + 1], o[mt][4 * i + 2], o[mt][4 * i + 3]};
+                    *reinterpret_cast<floatx4 *>(dst + d) = t;
+                }
+            }
+        if (hh == 0) {
+            mb[w * 32 + c] = m;
+            lb[w * 32 + c] = lt;
+        }
+    }
+    __syncthreads();
+
+    constexpr int DC = D / 4;
+    for (int u = tid; u < C::BM * DC; u += C::NT) {
+        const int qi = u / DC, ch = u % DC;
+        const int row = q0 + qi;
+        if (row >= S) continue;
+        const int base = (qi / 32) * NS * 32 + (qi % 32);  // wave (qg, 0), query qi%32
+        float ms = neg_inf();
+#pragma unroll
+        for (int j = 0; j < NS; ++j) ms = fmaxf(ms, mb[base + 32 * j]);
+        floatx4 accv = {0.f, 0.f, 0.f, 0.f};
+        float den = 0.f;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            const float mj = mb[base + 32 * j];
+            const float wgt = (NS == 1) ? 1.f : __builtin_amdgcn_exp2f(mj - ms);
+            den += wgt * lb[base + 32 * j];
+            const floatx4 oj = *reinterpret_cast<const floatx4 *>(ob + (base + 32 * j) * C::OP + 4 * ch);
+            accv += wgt * oj;
+        }
+        floatx4 res = {accv[0] / den, accv[1] / den, accv[2] / den, accv[3] / den};
+        store4<VEC>(obase + (size_t)row * ors + 4 * ch, res);
+    }
+}
+
+}  // namespace
+
+#define NC_FLASH_KERNEL(NAME, D, NQ, NS, CAUSAL, VEC)                                   \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) { \
+        flash_fwd_body<D, NQ, NS, CAUSAL, VEC>(a);                                      \
+    }
+
+// 16-byte vector variants: block_m = 128 (4 query waves), 64 (2 x 2 key splits), 32 (4 key splits).
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m128_full, 16, 4, 1, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m128_causal, 16, 4, 1, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_full, 16, 2, 2, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_causal, 16, 2, 2, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m32_full, 16, 1, 4, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m32_causal, 16, 1, 4, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m128_full, 32, 4, 1, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m128_causal, 32, 4, 1, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_full, 32, 2, 2, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_causal, 32, 2, 2, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m32_full, 32, 1, 4, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m32_causal, 32, 1, 4, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m128_full, 64, 4, 1, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m128_causal, 64, 4, 1, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_full, 64, 2, 2, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_causal, 64, 2, 2, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m32_full, 64, 1, 4, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m32_causal, 64, 1, 4, true, true)
+
+// Element-wise variants for slices whose base or strides break 16-byte alignment.
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_full_unaligned, 16, 2, 2, false, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_causal_unaligned, 16, 2, 2, true, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_full_unaligned, 32, 2, 2, false, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_causal_unaligned, 32, 2, 2, true, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_full_unaligned, 64, 2, 2, false, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_causal_unaligned, 64, 2, 2, true, false)
+
+// Plain 16-byte copy, used only to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte
+// count (bench.py --calibrate-copy).
+extern "C" __global__ __launch_bounds__(256) void nc_util_copy_b128(const u32x4 *src, u32x4 *dst, uint64_t n16) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256ull) dst[i] = src[i];
+}

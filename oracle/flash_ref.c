@@ -1,0 +1,215 @@
+/*
+ * flash_ref.c — CPU restatement of not-cute-zig's flash-attention oracle.
+ *
+ * TEST INFRASTRUCTURE. This file is the checker for the gfx950 kernels: only tests/, the smoke
+ * check in __graft_entry__.py and the cpu_baseline leg of bench.py may load it. It is never part of
+ * the product path and the product never falls back to it.
+ *
+ * Follows computeFlashReferenceOne (/root/reference/src/main.zig:1271-1307), called per slice as in
+ * computeFlashReference / computeFlashReferenceSlices (src/main.zig:1213-1269):
+ *   for each row:
+ *     score[key] = (sum_kk f32(q[row][kk]) * f32(k[key][kk])) * scale   (f32, kk in order, no FMA)
+ *     masked (causal and key > row) -> -inf; row_max over the visible scores      (:1276-1289)
+ *     weight[key] = masked ? 0 : exp(score - row_max); row_sum += weight, keys in order (:1291-1296)
+ *     o[row][c] = sum_key (weight[key] / row_sum) * f32(v[key][c]), keys in order  (:1298-1305)
+ * Generalised with a row stride per tensor (0 = head_dim, the reference layout). Only the active
+ * rows x head_dim region of each O slice is written; padding keeps whatever the caller put there.
+ *
+ * Two rearrangements keep every result bit-identical to the loop nest above while making it fast
+ * enough for the large configurations: (1) weight[key] / row_sum is computed once per key instead of
+ * once per (key, column) — IEEE division is deterministic, so the product term is the same value;
+ * (2) the column loop is moved inside the key loop — every o[row][c] still sums over keys in the
+ * same order. Build with -ffp-contract=off and without -ffast-math so no multiply-add is fused and
+ * no sum is reassociated.
+ *
+ * Parity pins (tests/test_oracle.py): golden vectors from an independent float64 numpy softmax
+ * (tests/golden/make_golden.py), closed forms (constant V, scale 0, causal row 0, equal keys,
+ * dominant key), invariants (key permutation, slice independence, padding untouched, causal prefix
+ * dependence) and the reference's own smoke-case fills.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+static float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    uint32_t x;
+    if (e == 0x1f) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else if (e != 0) {
+        x = sign | ((e + 112) << 23) | (m << 13);
+    } else if (m == 0) {
+        x = sign;
+    } else {
+        uint32_t ex = 113;
+        while ((m & 0x400u) == 0) {
+            m <<= 1;
+            --ex;
+        }
+        x = sign | (ex << 23) | ((m & 0x3ffu) << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+float oracle_half_to_float(uint16_t h) { return half_to_float(h); }
+
+typedef struct {
+    int64_t S, D;
+    const float *q;  /* [S][D] */
+    const float *kt; /* [D][S]  (transposed so the key loop is contiguous) */
+    const float *v;  /* [S][D] */
+    float *o;        /* slice base */
+    int64_t o_row;
+    float scale;
+    int causal;
+} slice_ctx;
+
+/* One row of computeFlashReferenceOne (src/main.zig:1272-1306). `scores` has S floats, `acc` D. */
+static void oracle_row(const slice_ctx *c, int64_t row, float *scores, float *acc) {
+    const int64_t S = c->S, D = c->D;
+    const float neg_inf = -INFINITY;
+    float row_max = neg_inf;
+    const float *qr = c->q + row * D;
+    /* scores for visible keys, 8 keys at a time; each key's dot product is summed in kk order */
+    const int64_t visible = c->causal ? row + 1 : S;
+    int64_t key = 0;
+    for (; key + 8 <= visible; key += 8) {
+        float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int64_t kk = 0; kk < D; ++kk) {
+            const float qv = qr[kk];
+            const float *kr = c->kt + kk * S + key;
+            for (int j = 0; j < 8; ++j) s8[j] += qv * kr[j];
+        }
+        for (int j = 0; j < 8; ++j) scores[key + j] = s8[j] * c->scale;
+    }
+    for (; key < visible; ++key) {
+        float s = 0.f;
+        for (int64_t kk = 0; kk < D; ++kk) s += qr[kk] * c->kt[kk * S + key];
+        scores[key] = s * c->scale;
+    }
+    for (key = 0; key < visible; ++key) row_max = fmaxf(row_max, scores[key]);
+    for (key = visible; key < S; ++key) scores[key] = neg_inf;
+
+    float row_sum = 0.f;
+    for (key = 0; key < S; ++key) {
+        const float w = (scores[key] == neg_inf) ? 0.f : expf(scores[key] - row_max);
+        scores[key] = w;
+        row_sum += w;
+    }
+    for (int64_t col = 0; col < D; ++col) acc[col] = 0.f;
+    for (key = 0; key < S; ++key) {
+        const float w = scores[key] / row_sum;
+        const float *vr = c->v + key * D;
+        for (int64_t col = 0; col < D; ++col) acc[col] += w * vr[col];
+    }
+    float *orow = c->o + row * c->o_row;
+    for (int64_t col = 0; col < D; ++col) orow[col] = acc[col];
+}
+
+typedef struct {
+    const slice_ctx *ctx;
+    const int64_t *rows; /* NULL: rows 0..S-1 */
+    int64_t nrows;
+    int64_t next;        /* shared work counter */
+    pthread_mutex_t lock;
+} row_pool;
+
+static void *row_worker(void *arg) {
+    row_pool *p = (row_pool *)arg;
+    float *scores = (float *)malloc(sizeof(float) * (size_t)p->ctx->S);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)p->ctx->D);
+    if (!scores || !acc) {
+        free(scores);
+        free(acc);
+        return (void *)1;
+    }
+    for (;;) {
+        pthread_mutex_lock(&p->lock);
+        const int64_t begin = p->next;
+        p->next += 16;
+        pthread_mutex_unlock(&p->lock);
+        if (begin >= p->nrows) break;
+        const int64_t end = begin + 16 < p->nrows ? begin + 16 : p->nrows;
+        for (int64_t i = begin; i < end; ++i) oracle_row(p->ctx, p->rows ? p->rows[i] : i, scores, acc);
+    }
+    free(scores);
+    free(acc);
+    return NULL;
+}
+
+/*
+ * Attention forward over batch_heads slices. Strides are in elements; row strides of 0 mean
+ * head_dim. rows == NULL computes every row; otherwise only rows[0..nrows) of every slice (each
+ * must be < seq_len). threads <= 1 runs on the calling thread. Returns 0, or -1 on bad arguments or
+ * allocation failure.
+ */
+int oracle_flash_fwd(uint64_t batch_heads, uint64_t seq_len, uint64_t head_dim, const uint16_t *q,
+                     uint64_t q_stride, uint64_t q_row, const uint16_t *k, uint64_t k_stride, uint64_t k_row,
+                     const uint16_t *v, uint64_t v_stride, uint64_t v_row, float *o, uint64_t o_stride,
+                     uint64_t o_row, float scale, uint32_t causal, int threads, const int64_t *rows,
+                     uint64_t nrows) {
+    if (!q || !k || !v || !o || seq_len == 0 || head_dim == 0) return -1;
+    const int64_t S = (int64_t)seq_len, D = (int64_t)head_dim;
+    if (!q_row) q_row = head_dim;
+    if (!k_row) k_row = head_dim;
+    if (!v_row) v_row = head_dim;
+    if (!o_row) o_row = head_dim;
+    if (rows)
+        for (uint64_t i = 0; i < nrows; ++i)
+            if (rows[i] < 0 || rows[i] >= S) return -1;
+    float *qf = (float *)malloc(sizeof(float) * (size_t)(S * D));
+    float *kt = (float *)malloc(sizeof(float) * (size_t)(S * D));
+    float *vf = (float *)malloc(sizeof(float) * (size_t)(S * D));
+    if (!qf || !kt || !vf) {
+        free(qf);
+        free(kt);
+        free(vf);
+        return -1;
+    }
+    int rc = 0;
+    for (uint64_t b = 0; b < batch_heads && rc == 0; ++b) {
+        const uint16_t *qs = q + b * q_stride, *ks = k + b * k_stride, *vs = v + b * v_stride;
+        for (int64_t r = 0; r < S; ++r)
+            for (int64_t c = 0; c < D; ++c) {
+                qf[r * D + c] = half_to_float(qs[r * (int64_t)q_row + c]);
+                kt[c * S + r] = half_to_float(ks[r * (int64_t)k_row + c]);
+                vf[r * D + c] = half_to_float(vs[r * (int64_t)v_row + c]);
+            }
+        slice_ctx ctx = {S, D, qf, kt, vf, o + b * o_stride, (int64_t)o_row, scale, causal != 0};
+        row_pool pool;
+        pool.ctx = &ctx;
+        pool.rows = rows;
+        pool.nrows = rows ? (int64_t)nrows : S;
+        pool.next = 0;
+        pthread_mutex_init(&pool.lock, NULL);
+        if (threads <= 1) {
+            if (row_worker(&pool) != NULL) rc = -1;
+        } else {
+            pthread_t *tids = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+            int started = 0;
+            if (!tids) rc = -1;
+            for (int t = 0; t < threads && tids; ++t) {
+                if (pthread_create(&tids[t], NULL, row_worker, &pool) != 0) break;
+                ++started;
+            }
+            if (tids && started == 0) rc = row_worker(&pool) != NULL ? -1 : 0;
+            for (int t = 0; t < started; ++t) {
+                void *ret = NULL;
+                pthread_join(tids[t], &ret);
+                if (ret != NULL) rc = -1;
+            }
+            free(tids);
+        }
+        pthread_mutex_destroy(&pool.lock);
+    }
+    free(qf);
+    free(kt);
+    free(vf);
+    return rc;
+}

@@ -1,0 +1,236 @@
+"""Pins the CPU oracle (oracle/flash_ref.c) before it is trusted as the parity reference.
+
+1. Golden vectors: an independent float64 softmax(QK^T)V (tests/golden/make_golden.py).
+2. Closed forms: constant V, scale 0 (uniform weights), causal row 0, equal keys, a dominant key.
+3. Invariants: key/value permutation, slice independence, padding untouched, causal prefix
+   dependence, thread-count and row-subset determinism.
+4. Teeth: plausible mistakes (swapped K/V, transposed Q/K roles, dropped mask, wrong scale, dropped
+   last key) made in the oracle's call on the CPU each fail the golden check.
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+
+import flash_oracle
+import flashcheck as fc
+from flash_workloads import CONFIGS, Workload, reference_smoke_cases
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "flash_golden.npz")
+GOLD_TOL = 1e-5
+
+
+def _golden_cases():
+    z = np.load(GOLDEN, allow_pickle=False)
+    out = []
+    for name in z["names"]:
+        name = str(name)
+        p = z[f"{name}/params"]
+        out.append(dict(name=name, q=z[f"{name}/q"], k=z[f"{name}/k"], v=z[f"{name}/v"],
+                        o=z[f"{name}/o_expected"], bh=int(p[0]), s=int(p[1]), d=int(p[2]), causal=bool(p[3]),
+                        strides=[int(x) for x in p[4:8]], rows=[int(x) for x in p[8:12]],
+                        scale=float(z[f"{name}/scale"][0])))
+    return out
+
+
+GOLDEN_CASES = _golden_cases()
+
+
+def run_oracle(g, q=None, k=None, v=None, causal=None, scale=None, seq_len=None, threads=1):
+    o = np.full(g["o"].size, fc.SENTINEL, dtype=np.float32)
+    qs, ks, vs, os_ = g["strides"]
+    qr, kr, vr, orr = g["rows"]
+    flash_oracle.flash_fwd(g["q"] if q is None else q, g["k"] if k is None else k, g["v"] if v is None else v, o,
+                           batch_heads=g["bh"], seq_len=g["s"] if seq_len is None else seq_len, head_dim=g["d"],
+                           q_stride=qs, k_stride=ks, v_stride=vs, o_stride=os_,
+                           scale=g["scale"] if scale is None else scale,
+                           causal=g["causal"] if causal is None else causal, q_row=qr, k_row=kr, v_row=vr,
+                           o_row=orr, threads=threads)
+    return o
+
+
+def golden_error(g, o):
+    act = ~np.isnan(g["o"])
+    return float(np.max(np.abs(o[act].astype(np.float64) - g["o"][act])))
+
+
+@pytest.mark.parametrize("g", GOLDEN_CASES, ids=lambda g: g["name"])
+def test_oracle_matches_float64_golden(g):
+    o = run_oracle(g)
+    assert golden_error(g, o) <= GOLD_TOL
+    pads = np.isnan(g["o"])
+    assert np.all(o[pads] == fc.SENTINEL)
+
+
+@pytest.mark.parametrize("g", GOLDEN_CASES, ids=lambda g: g["name"])
+def test_golden_check_has_teeth(g):
+    """Each planted mistake moves the oracle far outside the golden tolerance."""
+    mistakes = {
+        "swap_k_v": dict(k=g["v"], v=g["k"]) if g["strides"][1] == g["strides"][2] and g["rows"][1] == g["rows"][2]
+        else None,
+        "wrong_scale": dict(scale=g["scale"] * 1.25),
+        "mask_flipped": dict(causal=not g["causal"]),
+        "q_k_roles_swapped": dict(q=g["k"], k=g["q"]) if g["strides"][0] == g["strides"][1] and
+        g["rows"][0] == g["rows"][1] else None,
+    }
+    for what, kw in mistakes.items():
+        if kw is None:
+            continue
+        o = run_oracle(g, **kw)
+        assert golden_error(g, o) > 100 * GOLD_TOL, what
+
+
+def _wl(bh, s, d, causal, scale, dists, seed=0, **kw):
+    return Workload("t", bh, s, d, causal, scale, dists, seed=seed, **kw)
+
+
+def test_constant_v_gives_constant_output():
+    wl = _wl(2, 45, 32, True, 0.2, (("normal", 0, 1), ("normal", 0, 1), ("uniform", 0, 0)), seed=3)
+    q, k, _ = wl.make_inputs()
+    v = np.full(wl.length("v"), np.float16(0.75).view(np.uint16), dtype=np.uint16)
+    o = fc.oracle(wl, q, k, v)
+    idx = fc.active_index(wl)
+    assert np.max(np.abs(o[idx] - 0.75)) <= 2e-6
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_zero_scale_is_mean_of_v(causal):
+    wl = _wl(1, 37, 16, causal, 0.0, (("normal", 0, 1),) * 3, seed=5)
+    q, k, v = wl.make_inputs()
+    o = fc.oracle(wl, q, k, v)[: 37 * 16].reshape(37, 16)
+    V = v[: 37 * 16].view(np.float16).astype(np.float64).reshape(37, 16)
+    if causal:
+        want = np.cumsum(V, axis=0) / np.arange(1, 38)[:, None]
+    else:
+        want = np.broadcast_to(V.mean(axis=0), V.shape)
+    assert np.max(np.abs(o - want)) <= 5e-6
+
+
+def test_causal_row_zero_is_v_row_zero():
+    wl = _wl(3, 50, 64, True, 0.125, (("normal", 0, 2),) * 3, seed=8)
+    q, k, v = wl.make_inputs()
+    o = fc.oracle(wl, q, k, v)
+    for b in range(3):
+        got = o[b * wl.stride("o"): b * wl.stride("o") + 64]
+        want = v[b * wl.stride("v"): b * wl.stride("v") + 64].view(np.float16).astype(np.float32)
+        assert np.array_equal(got, want)
+
+
+def test_equal_keys_give_prefix_means():
+    wl = _wl(1, 29, 32, True, 0.5, (("normal", 0, 1),) * 3, seed=9)
+    q, k, v = wl.make_inputs()
+    k = np.tile(k[:32], 29)
+    o = fc.oracle(wl, q, k, v).reshape(29, 32)
+    V = v.view(np.float16).astype(np.float64).reshape(29, 32)
+    assert np.max(np.abs(o - np.cumsum(V, axis=0) / np.arange(1, 30)[:, None])) <= 5e-6
+
+
+def test_dominant_key_selects_its_value():
+    s, d = 24, 32
+    wl = _wl(1, s, d, False, 1.0, (("normal", 0, 1),) * 3, seed=10)
+    _, _, v = wl.make_inputs()
+    k = np.zeros((s, d), dtype=np.float16)
+    for key in range(s):
+        k[key, key % d] = 1.0
+    q = np.zeros((s, d), dtype=np.float16)
+    target = (np.arange(s) * 7 + 3) % s
+    for row in range(s):
+        q[row, target[row] % d] = 30.0  # score 30 for the target key, 0 for the others
+    o = fc.oracle(wl, q.view(np.uint16).ravel(), k.view(np.uint16).ravel(), v).reshape(s, d)
+    V = v.view(np.float16).astype(np.float32).reshape(s, d)
+    assert np.max(np.abs(o - V[target])) <= 1e-9 * s * 4 + 1e-6
+
+
+def test_key_value_permutation_invariance():
+    wl = _wl(1, 40, 32, False, 0.3, (("normal", 0, 1),) * 3, seed=11)
+    q, k, v = wl.make_inputs()
+    perm = np.random.default_rng(0).permutation(40)
+    k2 = k.reshape(40, 32)[perm].ravel()
+    v2 = v.reshape(40, 32)[perm].ravel()
+    a = fc.oracle(wl, q, k, v)
+    b = fc.oracle(wl, q, k2, v2)
+    assert np.max(np.abs(a - b)) <= 2e-6
+
+
+def test_slices_are_independent():
+    wl = _wl(4, 33, 16, True, 0.25, (("normal", 0, 1),) * 3, seed=12)
+    q, k, v = wl.make_inputs()
+    full = fc.oracle(wl, q, k, v)
+    one = _wl(1, 33, 16, True, 0.25, wl.dists)
+    n = 33 * 16
+    for b in range(4):
+        sl = slice(b * n, (b + 1) * n)
+        single = fc.oracle(one, q[sl].copy(), k[sl].copy(), v[sl].copy())
+        assert np.array_equal(full[sl].view(np.uint32), single.view(np.uint32))
+
+
+def test_causal_rows_depend_only_on_prefix():
+    wl = _wl(1, 48, 32, True, 0.2, (("normal", 0, 1),) * 3, seed=13)
+    q, k, v = wl.make_inputs()
+    a = fc.oracle(wl, q, k, v)
+    k2, v2 = k.copy(), v.copy()
+    k2[20 * 32:] = np.float16(5.0).view(np.uint16)
+    v2[20 * 32:] = np.float16(-3.0).view(np.uint16)
+    b = fc.oracle(wl, q, k2, v2)
+    assert np.array_equal(a[: 20 * 32].view(np.uint32), b[: 20 * 32].view(np.uint32))
+    assert not np.array_equal(a[20 * 32:], b[20 * 32:])
+
+
+def test_padding_untouched_and_threads_and_rows_deterministic():
+    for wl in reference_smoke_cases() + [CONFIGS["c2_causal"]]:
+        q, k, v = wl.make_inputs()
+        o1 = fc.oracle(wl, q, k, v, threads=1)
+        o8 = fc.oracle(wl, q, k, v, threads=8)
+        assert np.array_equal(o1.view(np.uint32), o8.view(np.uint32))
+        mask = np.ones(o1.size, dtype=bool)
+        mask[fc.active_index(wl)] = False
+        assert np.all(o1[mask] == fc.SENTINEL)
+        rows = [0, wl.seq_len // 2, wl.seq_len - 1]
+        orow = fc.oracle(wl, q, k, v, rows=rows)
+        idx = fc.active_index(wl, rows)
+        assert np.array_equal(orow[idx].view(np.uint32), o1[idx].view(np.uint32))
+
+
+def test_reference_smoke_fill_pattern():
+    """fillFlashInput (src/main.zig:1207-1211) via the library matches the formula in numpy."""
+    import notcute_flash as nc
+
+    for mul, add, scale in ((3, 1, 0.125), (5, 2, 0.0625), (7, 3, 0.03125)):
+        got = nc.fill_flash_input(1000, mul, add, scale)
+        i = np.arange(1000)
+        want = (((i * mul + add) % 17).astype(np.float32) * np.float32(scale)).astype(np.float16).view(np.uint16)
+        assert np.array_equal(got, want)
+
+
+def test_oracle_half_conversion_exhaustive():
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([flash_oracle.half_to_float(int(x)) for x in h[::7]], dtype=np.float32)
+    w = want[::7]
+    nan = np.isnan(w)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), w[~nan].view(np.uint32))
+
+
+def test_full_configs_match_float64_on_sampled_rows():
+    """c3 (headline) and c5 (large logits) against float64 on a few rows: the oracle stays within
+    1e-5 of the exact value where the GPU is held to 2e-3."""
+    for name in ("c3",):
+        wl = CONFIGS[name]
+        q, k, v = wl.make_inputs()
+        rows = [0, 1, 511, 1023]
+        o = fc.oracle(wl, q, k, v, rows=rows)
+        d = wl.head_dim
+        for b in (0, wl.batch_heads - 1):
+            Q = q[b * wl.stride("q"):][: wl.seq_len * d].view(np.float16).astype(np.float64).reshape(-1, d)
+            K = k[b * wl.stride("k"):][: wl.seq_len * d].view(np.float16).astype(np.float64).reshape(-1, d)
+            V = v[b * wl.stride("v"):][: wl.seq_len * d].view(np.float16).astype(np.float64).reshape(-1, d)
+            for r in rows:
+                sc = (K[: r + 1] @ Q[r]) * float(np.float32(wl.scale))
+                p = np.exp(sc - sc.max())
+                want = (p / p.sum()) @ V[: r + 1]
+                got = o[b * wl.stride("o") + r * d:][:d]
+                assert np.max(np.abs(got - want)) <= 1e-5
+    assert math.isfinite(GOLD_TOL)
