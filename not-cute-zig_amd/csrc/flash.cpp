@@ -20,69 +20,63 @@
 
 namespace {
 
-// Geometry of one nc_flash_fwd_* kernel; must agree with Cfg<> in flash_fwd.hip.
-struct Geometry {
-    uint32_t nq, ns;  // query waves, key-split waves
-    uint32_t bm() const { return 32 * nq; }
-    uint32_t bn() const { return 32 * ns; }
-    uint32_t threads() const { return 64 * nq * ns; }
-    uint32_t lds_bytes(uint32_t d) const {
-        const uint32_t nw = nq * ns;
-        const uint32_t dv = d < 32 ? 32 : d;
-        const uint32_t k_bytes = bn() * (d + 8) * 2;
-        const uint32_t v_bytes = dv * (bn() + 8) * 2;
-        const uint32_t o_bytes = nw * 32 * (d + 4) * 4;
-        const uint32_t stage = k_bytes + v_bytes;
-        return (stage > o_bytes ? stage : o_bytes) + nw * 32 * 2 * 4;
-    }
-};
+// Kernel families of flash_fwd.hip. Geometry and LDS sizes must agree with Cfg<> / PipeCfg<>.
+enum class Family { kPipe, kGeneric };
 
 struct Variant {
     const char *name;
     uint32_t d;
-    uint32_t bm;
+    uint32_t nq;      // query waves (32 rows each)
+    uint32_t ns;      // key-split waves
+    uint32_t nstage;  // LDS ring depth (pipelined family)
     bool causal;
     bool aligned;
+    Family family;
+
+    uint32_t bm() const { return 32 * nq; }
+    uint32_t bn() const { return 32 * ns; }
+    uint32_t threads() const { return 64 * nq * ns; }
+    uint32_t lds_bytes() const {
+        const uint32_t nw = nq * ns;
+        const uint32_t o_bytes = nw * 32 * (d + 4) * 4;
+        if (family == Family::kPipe) {
+            const uint32_t ring = nstage * 2 * bn() * d * 2;
+            return (ring > o_bytes ? ring : o_bytes) + 16 + nw * 32 * 2 * 4;
+        }
+        const uint32_t dv = d < 32 ? 32 : d;
+        const uint32_t stage = bn() * (d + 8) * 2 + dv * (bn() + 8) * 2;
+        return (stage > o_bytes ? stage : o_bytes) + nw * 32 * 2 * 4;
+    }
 };
+
+#define PIPE(D, NQ, NS, P, C) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "_" C, D, NQ, NS, P, \
+                               C[0] == 'c', true, Family::kPipe}
+#define GEN(D, C, A, SUF) {"nc_flash_fwd_d" #D "_m64_" C SUF, D, 2, 2, 1, C[0] == 'c', A, Family::kGeneric}
 
 const Variant kVariants[] = {
-    {"nc_flash_fwd_d16_m128_full", 16, 128, false, true},
-    {"nc_flash_fwd_d16_m128_causal", 16, 128, true, true},
-    {"nc_flash_fwd_d16_m64_full", 16, 64, false, true},
-    {"nc_flash_fwd_d16_m64_causal", 16, 64, true, true},
-    {"nc_flash_fwd_d16_m32_full", 16, 32, false, true},
-    {"nc_flash_fwd_d16_m32_causal", 16, 32, true, true},
-    {"nc_flash_fwd_d32_m128_full", 32, 128, false, true},
-    {"nc_flash_fwd_d32_m128_causal", 32, 128, true, true},
-    {"nc_flash_fwd_d32_m64_full", 32, 64, false, true},
-    {"nc_flash_fwd_d32_m64_causal", 32, 64, true, true},
-    {"nc_flash_fwd_d32_m32_full", 32, 32, false, true},
-    {"nc_flash_fwd_d32_m32_causal", 32, 32, true, true},
-    {"nc_flash_fwd_d64_m128_full", 64, 128, false, true},
-    {"nc_flash_fwd_d64_m128_causal", 64, 128, true, true},
-    {"nc_flash_fwd_d64_m64_full", 64, 64, false, true},
-    {"nc_flash_fwd_d64_m64_causal", 64, 64, true, true},
-    {"nc_flash_fwd_d64_m32_full", 64, 32, false, true},
-    {"nc_flash_fwd_d64_m32_causal", 64, 32, true, true},
-    {"nc_flash_fwd_d16_m64_full_unaligned", 16, 64, false, false},
-    {"nc_flash_fwd_d16_m64_causal_unaligned", 16, 64, true, false},
-    {"nc_flash_fwd_d32_m64_full_unaligned", 32, 64, false, false},
-    {"nc_flash_fwd_d32_m64_causal_unaligned", 32, 64, true, false},
-    {"nc_flash_fwd_d64_m64_full_unaligned", 64, 64, false, false},
-    {"nc_flash_fwd_d64_m64_causal_unaligned", 64, 64, true, false},
+    PIPE(64, 8, 1, 3, "full"), PIPE(64, 8, 1, 3, "causal"), PIPE(64, 4, 1, 3, "full"), PIPE(64, 4, 1, 3, "causal"),
+    PIPE(64, 2, 4, 2, "full"), PIPE(64, 2, 4, 2, "causal"), PIPE(64, 1, 8, 2, "full"), PIPE(64, 1, 8, 2, "causal"),
+    PIPE(32, 4, 1, 3, "full"), PIPE(32, 4, 1, 3, "causal"), PIPE(32, 2, 4, 2, "full"), PIPE(32, 2, 4, 2, "causal"),
+    PIPE(32, 1, 8, 2, "full"), PIPE(32, 1, 8, 2, "causal"),
+    PIPE(16, 2, 4, 2, "full"), PIPE(16, 2, 4, 2, "causal"), PIPE(16, 1, 8, 2, "full"), PIPE(16, 1, 8, 2, "causal"),
+    GEN(16, "full", true, ""), GEN(16, "causal", true, ""), GEN(32, "full", true, ""), GEN(32, "causal", true, ""),
+    GEN(64, "full", true, ""), GEN(64, "causal", true, ""),
+    GEN(16, "full", false, "_unaligned"), GEN(16, "causal", false, "_unaligned"),
+    GEN(32, "full", false, "_unaligned"), GEN(32, "causal", false, "_unaligned"),
+    GEN(64, "full", false, "_unaligned"), GEN(64, "causal", false, "_unaligned"),
 };
+#undef PIPE
+#undef GEN
 
-Geometry geometry_for(uint32_t bm) {
-    switch (bm) {
-    case 128: return {4, 1};
-    case 64: return {2, 2};
-    default: return {1, 4};
-    }
+const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal) {
+    for (const auto &v : kVariants)
+        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.causal == causal) return &v;
+    return nullptr;
 }
 
-const Variant *find_variant(uint32_t d, uint32_t bm, bool causal, bool aligned) {
+const Variant *find_generic(uint32_t d, bool causal, bool aligned) {
     for (const auto &v : kVariants)
-        if (v.d == d && v.bm == bm && v.causal == causal && v.aligned == aligned) return &v;
+        if (v.family == Family::kGeneric && v.d == d && v.causal == causal && v.aligned == aligned) return &v;
     return nullptr;
 }
 
@@ -104,15 +98,19 @@ const char *reference_kernel(const nc_flash_options &o) {
     return "flash_attention_fwd_opt";
 }
 
-// MI355X block-size choice: prefer the 128-query block (4 waves share every staged K/V tile)
-// while the grid still gives every one of the 256 CUs two workgroups; otherwise shrink the query
-// block and split each block's keys over more waves, so short sequences still fill the chip.
-uint32_t choose_block_m(const nc_flash_options &o) {
+// MI355X dispatch (256 CUs). Wider query blocks share every staged K/V tile among more waves, so
+// they are preferred while the grid still gives every CU at least one workgroup; short or few
+// sequences move to narrower query blocks whose keys are split over more waves, so that even the
+// heaviest (causal: last) query block finishes in a few key-block steps.
+const Variant *choose_pipe(const nc_flash_options &o) {
     constexpr uint64_t kCUs = 256;
+    const uint32_t d = (uint32_t)o.head_dim;
+    const bool causal = o.causal != 0;
     auto wgs = [&](uint64_t bm) { return ((o.seq_len + bm - 1) / bm) * o.batch_heads; };
-    if (wgs(128) >= 2 * kCUs) return 128;
-    if (wgs(64) >= kCUs) return 64;
-    return 32;
+    if (d == 64 && wgs(256) >= kCUs) return find_pipe(d, 8, 1, causal);
+    if (d >= 32 && wgs(128) >= kCUs) return find_pipe(d, 4, 1, causal);
+    if (wgs(64) >= kCUs) return find_pipe(d, 2, 4, causal);
+    return find_pipe(d, 1, 8, causal);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -123,32 +121,35 @@ int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selec
     if (st) return st;
     const nc_flash_options &o = *opts;
     const uint64_t d = o.head_dim;
+    const uint64_t rows[4] = {row_stride_of(o.q_row_stride, d), row_stride_of(o.k_row_stride, d),
+                              row_stride_of(o.v_row_stride, d), row_stride_of(o.o_row_stride, d)};
     // 16-byte vector path: every Q/K/V row start is 16-byte aligned and O rows are float4 aligned.
     const bool strides_ok = o.q_stride % 8 == 0 && o.k_stride % 8 == 0 && o.v_stride % 8 == 0 &&
-                            o.o_stride % 4 == 0 && row_stride_of(o.q_row_stride, d) % 8 == 0 &&
-                            row_stride_of(o.k_row_stride, d) % 8 == 0 &&
-                            row_stride_of(o.v_row_stride, d) % 8 == 0 &&
-                            row_stride_of(o.o_row_stride, d) % 4 == 0;
+                            o.o_stride % 4 == 0 && rows[0] % 8 == 0 && rows[1] % 8 == 0 && rows[2] % 8 == 0 &&
+                            rows[3] % 4 == 0;
     const bool aligned = vec_ok && strides_ok;
-    const uint32_t bm = aligned ? choose_block_m(o) : 64;
-    const Variant *v = find_variant((uint32_t)d, bm, o.causal != 0, aligned);
+    // The pipelined kernels address each Q/K/V slice with 32-bit buffer offsets, including up to
+    // one block (<= 256 rows) past seq_len.
+    uint64_t max_row = rows[0] > rows[1] ? rows[0] : rows[1];
+    max_row = max_row > rows[2] ? max_row : rows[2];
+    const bool offsets_fit = max_row < (1ull << 30) && (o.seq_len + 512) * max_row * 2 < (1ull << 31);
+    const Variant *v = (aligned && offsets_fit) ? choose_pipe(o) : find_generic((uint32_t)d, o.causal != 0, aligned);
     if (!v) return NC_ERROR_NOT_FOUND;
-    const Geometry g = geometry_for(bm);
-    const uint64_t nqb = (o.seq_len + bm - 1) / bm;
+    const uint64_t nqb = (o.seq_len + v->bm() - 1) / v->bm();
     uint64_t grid = 0;
     if (mul_overflows(nqb, o.batch_heads, &grid) || grid > 0xffffffffull) return NC_ERROR_OVERFLOW;
     std::memset(out, 0, sizeof *out);
     out->name = v->name;
     out->label = v->name;
     out->reference_name = reference_kernel(o);
-    out->threads = g.threads();
+    out->threads = v->threads();
     out->grid[0] = (uint32_t)grid;
     out->grid[1] = 1;
     out->grid[2] = 1;
-    out->block_m = g.bm();
-    out->block_n = g.bn();
-    out->kv_splits = g.ns;
-    out->lds_bytes = g.lds_bytes((uint32_t)d);
+    out->block_m = v->bm();
+    out->block_n = v->bn();
+    out->kv_splits = v->ns;
+    out->lds_bytes = v->lds_bytes();
     out->aligned = aligned ? 1u : 0u;
     return NC_SUCCESS;
 }

@@ -41,6 +41,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (P <= 2^8)
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
@@ -356,6 +357,353 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
     }
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// Pipelined variant (16-byte aligned rows, slices below 2 GiB): K and V stream through an
+// NSTAGE-deep LDS ring by direct buffer->LDS loads (buffer_load_dwordx4 ... lds), so no VGPRs or
+// ds_write instructions are spent on staging and NSTAGE-1 blocks are always in flight. The buffer
+// descriptors cover exactly each slice's active rows, so key rows past seq_len read as zero
+// without a branch. K and V keep their row-major layout in LDS with 16-byte chunks XOR-swizzled
+// per row against bank conflicts; the Q K^T A-operand is one ds_read_b128 per 16 head columns, and
+// the V^T A-operand of the PV product is assembled by ds_read_b64_tr_b16: inside each 16-lane group
+// lane m points at V[r0 + m/4][d0 + 4(m%4)], and lane i receives V[r0..r0+3][d0 + i].
+// One s_barrier per block (no fence): each wave first waits on its own loads of that block.
+// ---------------------------------------------------------------------------------------------
+
+#define NC_LDS(T) __attribute__((address_space(3))) T
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+template <int D>
+struct Swz {
+    static constexpr int CH = D / 8;  // 16-byte chunks per row
+    // slot of chunk ch in row r
+    __device__ static __forceinline__ int slot(int r, int ch) { return r * CH + (ch ^ ((r >> 1) & (CH - 1))); }
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// s_waitcnt vmcnt(n) with lgkmcnt(0), then a plain workgroup barrier (no memory fence, so loads of
+// later blocks stay in flight). The asm memory clobber keeps the compiler from moving LDS accesses
+// across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+    asm volatile("s_barrier" ::: "memory");
+}
+
+template <int LPW, int NSTAGE>
+__device__ __forceinline__ void wait_block(int ahead) {
+    // ahead = blocks issued after the one about to be consumed (0 .. NSTAGE-2)
+    if constexpr (NSTAGE >= 4) {
+        if (ahead >= 2) { wait_vm_barrier<2 * LPW>(); return; }
+    }
+    if constexpr (NSTAGE >= 3) {
+        if (ahead >= 1) { wait_vm_barrier<LPW>(); return; }
+    }
+    wait_vm_barrier<0>();
+}
+
+// An empty asm statement that consumes the K fragments: every compiler-issued K read has then
+// been waited for, so asm-issued LDS reads that follow never sit under a compiler lgkmcnt wait.
+template <int N>
+__device__ __forceinline__ void lds_reads_done(half8 (&k)[N]) {
+    if constexpr (N == 1) asm volatile("" ::"v"(k[0]));
+    else if constexpr (N == 2) asm volatile("" ::"v"(k[0]), "v"(k[1]));
+    else asm volatile("" ::"v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]));
+}
+
+// s_waitcnt lgkmcnt(0) that the compiler sees as producing the given registers, so no consumer of
+// an asm-issued LDS read can be scheduled before the wait.
+template <int MT>
+__device__ __forceinline__ void wait_lds_tied(u32x2 (&v)[MT][2][2]) {
+    if constexpr (MT == 1) {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0][0][0]), "+v"(v[0][0][1]), "+v"(v[0][1][0]), "+v"(v[0][1][1]));
+    } else {
+        static_assert(MT == 2, "head 64 at most");
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(v[0][0][0]), "+v"(v[0][0][1]), "+v"(v[0][1][0]), "+v"(v[0][1][1]),
+                       "+v"(v[1][0][0]), "+v"(v[1][0][1]), "+v"(v[1][1][0]), "+v"(v[1][1][1]));
+    }
+}
+
+template <int D, int NQ, int NS, int NSTAGE>
+struct PipeCfg {
+    static constexpr int NW = NQ * NS;
+    static constexpr int NT = NW * 64;
+    static constexpr int BM = 32 * NQ;
+    static constexpr int BN = 32 * NS;
+    static constexpr int CH = D / 8;
+    static constexpr int TILE = BN * D * 2;             // bytes of one K (or V) block
+    static constexpr int STAGE = 2 * TILE;
+    static constexpr int LOADS = 2 * BN * CH / 64;      // wave-level 16-byte load instructions per block
+    static_assert(LOADS % NW == 0, "every wave issues the same number of loads per block");
+    static constexpr int LPW = LOADS / NW;
+    static constexpr int RING = NSTAGE * STAGE;
+    static constexpr int OP = D + 4;
+    static constexpr int O_BYTES = NW * 32 * OP * 4;
+    static constexpr int ZERO_OFF = RING > O_BYTES ? RING : O_BYTES;
+    static constexpr int ML_OFF = ZERO_OFF + 16;
+    static constexpr int LDS_BYTES = ML_OFF + NW * 32 * 2 * 4;
+    static constexpr int MT = D < 32 ? 1 : D / 32;
+};
+
+template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE>
+__device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &a) {
+    using C = PipeCfg<D, NQ, NS, NSTAGE>;
+    using SW = Swz<D>;
+    static_assert(NSTAGE >= 2 && NSTAGE <= 4, "ring depth");
+    __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+
+    if (a.head_dim != (uint64_t)D || a.seq_len == 0) return;
+
+    const int S = (int)a.seq_len;
+    const uint32_t bh = a.batch_heads;
+    const uint32_t nqb = a.num_q_blocks;
+    const uint32_t L = blockIdx.x;
+    uint32_t head, qb_rev;
+    if ((bh & 7u) == 0) {
+        const uint32_t hpx = bh >> 3, x = L & 7u, idx = L >> 3;
+        head = x * hpx + idx % hpx;
+        qb_rev = idx / hpx;
+    } else {
+        head = L % bh;
+        qb_rev = L / bh;
+    }
+    const int qb = (int)(nqb - 1u - qb_rev);
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int c = lane & 31;
+    const int hh = lane >> 5;
+    const int qg = w / NS;
+    const int s = w % NS;
+    const int q0 = qb * C::BM;
+    const int qw0 = q0 + 32 * qg;
+    const int qrow = qw0 + c;
+    const int qw_last = min(qw0 + 31, S - 1);
+
+    const uint32_t qrb = (uint32_t)a.q_row_stride * 2, krb = (uint32_t)a.k_row_stride * 2;
+    const uint32_t vrb = (uint32_t)a.v_row_stride * 2;
+    const uint32_t qspan = (uint32_t)((S - 1) * (uint64_t)a.q_row_stride + D) * 2;
+    const uint32_t kspan = (uint32_t)((S - 1) * (uint64_t)a.k_row_stride + D) * 2;
+    const uint32_t vspan = (uint32_t)((S - 1) * (uint64_t)a.v_row_stride + D) * 2;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + (size_t)head * a.q_stride, qspan);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.k + (size_t)head * a.k_stride, kspan);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v + (size_t)head * a.v_stride, vspan);
+    float *obase = a.o + (size_t)head * a.o_stride;
+    const size_t ors = a.o_row_stride;
+
+    // Q^T B-operand (rows past seq_len read as zero).
+    half8 qf[D / 16];
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+        qf[kk] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                               qr, (uint32_t)qrow * qrb + (16 * kk + 8 * hh) * 2, 0, 0));
+
+    if (tid < 4) reinterpret_cast<uint32_t *>(smem + C::ZERO_OFF)[tid] = 0u;
+
+    const int kv_end = CAUSAL ? min(S, q0 + C::BM) : S;
+    const int nblk = (kv_end + C::BN - 1) / C::BN;
+
+    // Per-lane constant parts of the staging addresses: wave-instruction t of a block covers
+    // 16-byte slots [64t, 64t+64) of the K tile (t < LOADS/2) or of the V tile.
+    auto issue = [&](int blk) {
+        char *sbase = smem + (blk % NSTAGE) * C::STAGE;
+#pragma unroll
+        for (int n = 0; n < C::LPW; ++n) {
+            const int t = w + C::NW * n;
+            const bool isv = t >= C::LOADS / 2;
+            const int tt = isv ? t - C::LOADS / 2 : t;
+            const int p = tt * 64 + lane;
+            const int r = p / C::CH, sl = p % C::CH;
+            const int ch = sl ^ ((r >> 1) & (C::CH - 1));
+            const uint32_t key = (uint32_t)(blk * C::BN + r);
+            NC_LDS(void) *dst = (NC_LDS(void) *)(sbase + (isv ? C::TILE : 0) + tt * 1024);
+            if (isv)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, key * vrb + ch * 16, 0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, dst, 16, key * krb + ch * 16, 0, 0, 0);
+        }
+    };
+
+    // Lane-constant LDS byte offsets of the MFMA operand reads inside a stage.
+    //  K (A operand of S^T): row 32s + c, chunk 2kk + hh.
+    int koff[D / 16];
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) koff[kk] = SW::slot(32 * s + c, 2 * kk + hh) * 16;
+    //  V^T (A operand of O^T), per (mt, ks, hf): rows 32s + 16ks + 8hf + 4*hv + m/4, columns
+    //  32mt + 16cg + 4(m%4) .. +3, where the 16-lane group index is G = 2*hv + cg.
+    const int G = lane >> 4, m = lane & 15, hv = G >> 1, cg = G & 1;
+    int voff[C::MT][2][2];
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int r = 32 * s + 16 * ks + 8 * hf + 4 * hv + (m >> 2);
+                const int d = 32 * mt + 16 * cg + 4 * (m & 3);
+                voff[mt][ks][hf] = (d < D) ? C::TILE + SW::slot(r, d >> 3) * 16 + ((d >> 2) & 1) * 8
+                                           : -1;  // head 16: columns 16..31 of the padded tile are zero
+            }
+
+    // Log2-domain scale. A negative scale is applied by negating the resident Q operand (exact),
+    // a zero scale by a tiny positive one (every score then rounds to weight exp2(0) = 1, as with
+    // a zero scale), so the softmax below can assume sc > 0.
+    float sc = a.scale * kLog2e;
+    if (sc < 0.f) {
+        sc = -sc;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) qf[kk] = -qf[kk];
+    }
+    if (!(sc > 0.f) && sc == 0.f) sc = 1e-30f;
+    float mrow = neg_inf();
+    float l = 0.f;
+    floatx16 o[C::MT];
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt) o[mt] = floatx16{};
+
+#pragma unroll
+    for (int b = 0; b < NSTAGE - 1; ++b)
+        if (b < nblk) issue(b);
+
+    for (int blk = 0; blk < nblk; ++blk) {
+        wait_block<C::LPW, NSTAGE>(min(NSTAGE - 2, nblk - 1 - blk));
+        if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1);
+
+        const int kt0 = blk * C::BN + 32 * s;
+        bool run = kt0 < S;
+        if (CAUSAL) run = run && kt0 <= qw_last;
+        if (!run) continue;
+
+        const char *st = smem + (blk % NSTAGE) * C::STAGE;
+        floatx16 acc = floatx16{};
+        half8 kf[D / 16];
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+            kf[kk] = *reinterpret_cast<const half8 *>(st + koff[kk]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], acc, 0, 0, 0);
+        }
+        lds_reads_done<D / 16>(kf);
+        // V^T operands, issued once every K read of this sub-tile has landed (lds_reads_done
+        // orders them) so their latency hides behind the softmax. ds_read_b64_tr_b16 goes
+        // through asm: the builtin is treated as aliasing the in-flight buffer->LDS loads of later
+        // blocks, and the compiler would drain them (vmcnt(0)) before every read.
+        // wait_lds_tied() waits for these reads and ties the registers to that wait.
+        u32x2 vt[C::MT][2][2];
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int off = voff[mt][ks][hf];
+                    const uint32_t addr = (uint32_t)(uintptr_t)(off >= 0 ? st + off : smem + C::ZERO_OFF);
+                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(vt[mt][ks][hf]) : "v"(addr));
+                }
+
+        // Online softmax on raw scores (sc > 0): the tile max is taken before scaling, which is
+        // exact because rounding is monotonic, and scale + subtract fuse into one FMA. The running
+        // max only moves (and O, l are rescaled) when some lane's max grows by more than 2^8, so P
+        // stays <= 256 (exact in f16 range) and the 32-multiply O rescale is rare.
+        const bool need_mask = (kt0 + 32 > S) || (CAUSAL && kt0 + 31 > qw0);
+        if (need_mask) {
+            const int lim = CAUSAL ? min(qrow, S - 1) - kt0 : S - 1 - kt0;  // last visible key offset
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (8 * (r >> 2) + 4 * hh + (r & 3) > lim) acc[r] = neg_inf();
+        }
+        float tmax = fmaxf(fmaxf(acc[0], acc[1]), acc[2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) tmax = fmaxf(fmaxf(tmax, acc[r]), acc[r + 1]);
+        tmax = fmaxf(tmax, acc[15]);
+        const float m_tile = pair_max(tmax) * sc;
+        if (__builtin_amdgcn_ballot_w64(m_tile > mrow + kRescaleLog2)) {
+            const float m_new = fmaxf(mrow, m_tile);
+            const float alpha = __builtin_amdgcn_exp2f(mrow - (m_new == neg_inf() ? 0.f : m_new));
+            l *= alpha;
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt) o[mt] *= alpha;
+            mrow = m_new;
+        }
+        const float neg_m = (mrow == neg_inf()) ? 0.f : -mrow;
+        float p[16];
+        float psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], sc, neg_m));
+            psum += p[r];
+        }
+        l += psum;
+
+        half8 pf[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pf[ks][j] = (_Float16)p[8 * ks + j];
+
+        wait_lds_tied<C::MT>(vt);
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const u32x4 vv = {vt[mt][ks][0][0], vt[mt][ks][0][1], vt[mt][ks][1][0], vt[mt][ks][1][1]};
+                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, vv), pf[ks], o[mt], 0, 0, 0);
+            }
+    }
+
+    // Epilogue (all loads landed, all LDS reads done), as in flash_fwd_body.
+    wait_vm_barrier<0>();
+    float *ob = reinterpret_cast<float *>(smem);
+    float *mb = reinterpret_cast<float *>(smem + C::ML_OFF);
+    float *lb = mb + C::NW * 32;
+    const float lt = pair_sum(l);
+    {
+        float *dst = ob + (w * 32 + c) * C::OP;
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 32 * mt + 8 * i + 4 * hh;
+                if (d < D) {
+                    floatx4 t = {o[mt][4 * i], o[mt][4 * i + 1], o[mt][4 * i + 2], o[mt][4 * i + 3]};
+                    *reinterpret_cast<floatx4 *>(dst + d) = t;
+                }
+            }
+        if (hh == 0) {
+            mb[w * 32 + c] = mrow;
+            lb[w * 32 + c] = lt;
+        }
+    }
+    __syncthreads();
+    constexpr int DC = D / 4;
+    for (int u = tid; u < C::BM * DC; u += C::NT) {
+        const int qi = u / DC, ch = u % DC;
+        const int row = q0 + qi;
+        if (row >= S) continue;
+        const int base = (qi / 32) * NS * 32 + (qi % 32);
+        float ms = neg_inf();
+#pragma unroll
+        for (int j = 0; j < NS; ++j) ms = fmaxf(ms, mb[base + 32 * j]);
+        floatx4 accv = {0.f, 0.f, 0.f, 0.f};
+        float den = 0.f;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            const float mj = mb[base + 32 * j];
+            const float wgt = (NS == 1) ? 1.f : __builtin_amdgcn_exp2f(mj - ms);
+            den += wgt * lb[base + 32 * j];
+            const floatx4 oj = *reinterpret_cast<const floatx4 *>(ob + (base + 32 * j) * C::OP + 4 * ch);
+            accv += wgt * oj;
+        }
+        floatx4 res = {accv[0] / den, accv[1] / den, accv[2] / den, accv[3] / den};
+        *reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch) = res;
+    }
+}
+
 }  // namespace
 
 #define NC_FLASH_KERNEL(NAME, D, NQ, NS, CAUSAL, VEC)                                   \
@@ -363,25 +711,14 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
         flash_fwd_body<D, NQ, NS, CAUSAL, VEC>(a);                                      \
     }
 
-// 16-byte vector variants: block_m = 128 (4 query waves), 64 (2 x 2 key splits), 32 (4 key splits).
-NC_FLASH_KERNEL(nc_flash_fwd_d16_m128_full, 16, 4, 1, false, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d16_m128_causal, 16, 4, 1, true, true)
+// Generic variants (64-bit addressing, register staging): 16-byte aligned rows whose slices are
+// too large for the pipelined kernels' 32-bit buffer offsets.
 NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_full, 16, 2, 2, false, true)
 NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_causal, 16, 2, 2, true, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d16_m32_full, 16, 1, 4, false, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d16_m32_causal, 16, 1, 4, true, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d32_m128_full, 32, 4, 1, false, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d32_m128_causal, 32, 4, 1, true, true)
 NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_full, 32, 2, 2, false, true)
 NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_causal, 32, 2, 2, true, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d32_m32_full, 32, 1, 4, false, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d32_m32_causal, 32, 1, 4, true, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d64_m128_full, 64, 4, 1, false, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d64_m128_causal, 64, 4, 1, true, true)
 NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_full, 64, 2, 2, false, true)
 NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_causal, 64, 2, 2, true, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d64_m32_full, 64, 1, 4, false, true)
-NC_FLASH_KERNEL(nc_flash_fwd_d64_m32_causal, 64, 1, 4, true, true)
 
 // Element-wise variants for slices whose base or strides break 16-byte alignment.
 NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_full_unaligned, 16, 2, 2, false, false)
@@ -396,3 +733,28 @@ NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_causal_unaligned, 64, 2, 2, true, false)
 extern "C" __global__ __launch_bounds__(256) void nc_util_copy_b128(const u32x4 *src, u32x4 *dst, uint64_t n16) {
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256ull) dst[i] = src[i];
 }
+
+#define NC_FLASH_PIPE_KERNEL(NAME, D, NQ, NS, CAUSAL, NSTAGE)                           \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) { \
+        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE>(a);                              \
+    }
+
+// Pipelined variants: q = query waves (32 rows each), s = key-split waves, p = LDS ring depth.
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q8s1p3_full, 64, 8, 1, false, 3)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q8s1p3_causal, 64, 8, 1, true, 3)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_full, 64, 4, 1, false, 3)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_causal, 64, 4, 1, true, 3)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_full, 64, 2, 4, false, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_causal, 64, 2, 4, true, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_full, 64, 1, 8, false, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_causal, 64, 1, 8, true, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_full, 32, 4, 1, false, 3)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_causal, 32, 4, 1, true, 3)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_full, 32, 2, 4, false, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_causal, 32, 2, 4, true, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p2_full, 32, 1, 8, false, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p2_causal, 32, 1, 8, true, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_full, 16, 2, 4, false, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_causal, 16, 2, 4, true, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_full, 16, 1, 8, false, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_causal, 16, 1, 8, true, 2)
