@@ -31,7 +31,7 @@ from flash_workloads import CONFIGS, HEADLINE  # noqa: E402
 
 PEAK_F16_TFLOPS = 2516.6  # 256 CU x 4096 flop/clk x 2.4 GHz, dense
 PEAK_HBM_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "flash_fwd_{workload}_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "flash_fwd_{workload}_traffic.txt")
 
 
 def log(msg: str) -> None:
@@ -184,7 +184,10 @@ def main() -> int:
     tf = TRAFFIC_FILE.format(workload=wl.name)
     if os.path.exists(tf):
         with open(tf) as f:
-            traffic = json.load(f).get("traffic_bytes_per_launch")
+            rec_t = json.load(f)
+        # only a figure measured on the kernel being timed is reported
+        if rec_t.get("kernel") == sel.name.decode():
+            traffic = rec_t.get("traffic_bytes_per_launch")
     if bound == "hbm":
         achieved = work["bytes"] / (ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",

@@ -1,0 +1,283 @@
+"""Host-side tests of the C ABI (no GPU calls): exported symbols, flash.Options validation
+(src/flash.zig:16-28), requireLen (src/flash.zig:98-100), the restated reference dispatch table
+(src/flash.zig:78-96), the MI355X dispatch geometry, the work model (src/main.zig:1032-1034), the
+benchmark arithmetic (src/benchmark.zig:80-89), error mapping (src/cuda.zig:134-178) and the CLI
+guard of bench.py."""
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import notcute_flash as nc
+from flash_workloads import CONFIGS
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "notcute_flash.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    lib = nc.load_library()
+    names = declared_functions()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_oracle_library_loads():
+    import flash_oracle
+
+    assert hasattr(flash_oracle.lib(), "oracle_flash_fwd")
+
+
+def test_product_does_not_import_oracle():
+    pkg = os.path.join(ROOT, "not-cute-zig_amd")
+    for fn in os.listdir(pkg):
+        if fn.endswith(".py"):
+            src = open(os.path.join(pkg, fn)).read()
+            assert "flash_oracle" not in src and "oracle/" not in src, fn
+
+
+def test_status_names_follow_cuda_error_order():
+    # CudaError members in declaration order, src/cuda.zig:134-151
+    ref = ["OutOfMemory", "Overflow", "SharedObjectInitFailed", "NotFound", "InvalidValue", "InvalidContext",
+           "InvalidDevice", "InvalidImage", "ContextIsDestroyed", "LaunchFailed", "LaunchOutOfResources",
+           "LaunchTimeout", "IllegalAddress", "NoDevice", "NotInitialized", "UnknownError"]
+    lib = nc.load_library()
+    assert lib.nc_status_name(0) == b"Success"
+    for i, name in enumerate(ref, start=1):
+        assert lib.nc_status_name(i).decode() == name
+    assert lib.nc_status_name(99) == b"UnknownError"
+
+
+def test_hip_error_mapping():
+    lib = nc.load_library()
+    # hipError_t values from hip_runtime_api.h
+    table = {0: "Success", 2: "OutOfMemory", 1: "InvalidValue", 100: "NoDevice", 3: "NotInitialized",
+             200: "InvalidImage", 303: "SharedObjectInitFailed", 500: "NotFound", 700: "IllegalAddress",
+             701: "LaunchOutOfResources", 702: "LaunchTimeout", 709: "ContextIsDestroyed", 719: "LaunchFailed",
+             101: "InvalidDevice", 201: "InvalidContext", 999: "UnknownError"}
+    for hip, name in table.items():
+        assert nc.STATUS_NAMES[lib.nc_status_from_hip(hip)] == name, hip
+
+
+def test_init_without_gpu_reports_no_device():
+    if nc.device_count() != 0:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(nc.NcError) as ei:
+        nc.init()
+    assert ei.value.name == "NoDevice"
+
+
+def _opts(**kw):
+    base = dict(batch_heads=2, seq_len=64, head_dim=32)
+    base.update(kw)
+    return nc.options(**base)
+
+
+def _status(o):
+    return nc.STATUS_NAMES[nc.load_library().nc_flash_validate(ctypes.byref(o))]
+
+
+def test_options_defaults_match_reference():
+    o = nc.FlashOptions()
+    nc.load_library().nc_flash_options_init(ctypes.byref(o))
+    assert o.batch_heads == 1 and o.causal == 0  # src/flash.zig:6,14
+    assert o.q_row_stride == o.k_row_stride == o.v_row_stride == o.o_row_stride == 0
+
+
+@pytest.mark.parametrize("d", [1, 8, 15, 16, 17, 31, 32, 33, 48, 63, 64, 65, 96, 128])
+def test_validate_head_dim(d):
+    want = "Success" if d in (16, 32, 64) else "InvalidValue"
+    assert _status(_opts(head_dim=d)) == want
+
+
+def test_validate_zero_batch_or_seq():
+    assert _status(_opts(batch_heads=0)) == "InvalidValue"
+    assert _status(_opts(seq_len=0)) == "InvalidValue"
+
+
+@pytest.mark.parametrize("which", ["q", "k", "v", "o"])
+def test_validate_slice_strides(which):
+    s, d = 64, 32
+    assert _status(_opts(**{f"{which}_stride": s * d})) == "Success"
+    assert _status(_opts(**{f"{which}_stride": s * d - 1})) == "InvalidValue"
+    assert _status(_opts(**{f"{which}_stride": s * d + 17})) == "Success"
+
+
+@pytest.mark.parametrize("which", ["q", "k", "v", "o"])
+def test_validate_row_strides(which):
+    s, d = 64, 32
+    # row stride below head_dim
+    assert _status(_opts(**{f"{which}_row_stride": d - 1, f"{which}_stride": 10 * s * d})) == "InvalidValue"
+    # padded rows need (S-1)*row + d elements per slice
+    row = 40
+    need = (s - 1) * row + d
+    assert _status(_opts(**{f"{which}_row_stride": row, f"{which}_stride": need})) == "Success"
+    assert _status(_opts(**{f"{which}_row_stride": row, f"{which}_stride": need - 1})) == "InvalidValue"
+
+
+def test_validate_overflow():
+    o = _opts(batch_heads=1 << 40, q_stride=1 << 30)
+    assert _status(o) == "Overflow"
+
+
+# The reference's selectKernel decisions at every boundary of src/flash.zig:83-95, hand-tabulated.
+REFERENCE_DISPATCH = [
+    # (d, S, BH, causal) -> reference kernel
+    ((16, 256, 8, False), "flash_attention_fwd_v2"),
+    ((16, 257, 8, False), "flash_attention_fwd_opt"),
+    ((32, 256, 9, True), "flash_attention_fwd_opt"),
+    ((32, 255, 8, True), "flash_attention_fwd_v2"),
+    ((64, 256, 8, False), "flash_attention_fwd_v2"),
+    ((64, 256, 8, True), "flash_attention_fwd_h64"),
+    ((64, 257, 8, False), "flash_attention_fwd_h64"),
+    ((64, 511, 8, False), "flash_attention_fwd_h64"),
+    ((64, 512, 8, False), "flash_attention_fwd_h64_bn32"),
+    ((64, 512, 1, True), "flash_attention_fwd_h64_bn32"),
+    ((64, 256, 9, False), "flash_attention_fwd_h64"),
+    ((64, 1024, 8, True), "flash_attention_fwd_h64_bn32"),
+    ((16, 4096, 64, True), "flash_attention_fwd_opt"),
+]
+
+
+@pytest.mark.parametrize("case,want", REFERENCE_DISPATCH)
+def test_reference_dispatch_table(case, want):
+    d, s, bh, causal = case
+    sel = nc.select_kernel(nc.options(batch_heads=bh, seq_len=s, head_dim=d, causal=causal))
+    assert sel.reference_name.decode() == want
+
+
+@pytest.mark.parametrize("d", [16, 32, 64])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("bh,s", [(1, 1), (1, 32), (8, 1024), (32, 4096), (64, 8192), (3, 333)])
+def test_dispatch_geometry(d, causal, bh, s):
+    sel = nc.select_kernel(nc.options(batch_heads=bh, seq_len=s, head_dim=d, causal=causal))
+    name = sel.name.decode()
+    assert f"_d{d}_" in name and name.endswith("_causal" if causal else "_full")
+    assert sel.threads % 64 == 0 and 64 <= sel.threads <= 1024
+    assert sel.grid[0] == -(-s // sel.block_m) * bh and sel.grid[1] == sel.grid[2] == 1
+    assert sel.block_m % 32 == 0 and sel.block_n == 32 * sel.kv_splits
+    assert sel.threads == 2 * sel.block_m * sel.kv_splits  # (block_m/32) query waves x splits x 64 lanes
+    assert 0 < sel.lds_bytes <= 160 * 1024
+    assert sel.aligned == 1
+
+
+def test_dispatch_headline_and_large_configs():
+    assert nc.select_kernel(CONFIGS["c3"].options()).name == b"nc_flash_fwd_d64_q1s8p2_causal"
+    assert nc.select_kernel(CONFIGS["c4"].options()).name == b"nc_flash_fwd_d64_q8s1p3_full"
+    assert nc.select_kernel(CONFIGS["c5"].options()).name == b"nc_flash_fwd_d64_q8s1p3_causal"
+
+
+def test_dispatch_alignment_fallbacks():
+    # odd slice pad (the reference's smoke strides): element-wise kernel
+    sel = nc.select_kernel(nc.options(batch_heads=2, seq_len=32, head_dim=32, q_stride=32 * 32 + 17,
+                                      k_stride=32 * 32 + 19, v_stride=32 * 32 + 23, o_stride=32 * 32 + 29,
+                                      causal=True))
+    assert sel.aligned == 0 and sel.name.decode().endswith("_unaligned")
+    # misaligned base pointer
+    o = nc.options(batch_heads=2, seq_len=64, head_dim=64)
+    assert nc.select_kernel_for(o, 4096 + 2, 4096, 4096, 4096).aligned == 0
+    assert nc.select_kernel_for(o, 4096, 4096, 4096, 4096).aligned == 1
+    # slices too large for 32-bit buffer offsets: generic 64-bit kernel
+    big = nc.options(batch_heads=1, seq_len=1 << 20, head_dim=64, q_row_stride=2048, k_row_stride=2048,
+                     v_row_stride=2048, q_stride=(1 << 20) * 2048, k_stride=(1 << 20) * 2048,
+                     v_stride=(1 << 20) * 2048)
+    sel = nc.select_kernel(big)
+    assert sel.aligned == 1 and "_m64_" in sel.name.decode()
+
+
+def test_pack_args_resolves_row_strides():
+    o = nc.options(batch_heads=3, seq_len=100, head_dim=32, q_row_stride=40, q_stride=100 * 40, scale=0.5,
+                   causal=True)
+    sel = nc.select_kernel(o)
+    a = nc.pack_args(o, sel, 0x1000, 0x2000, 0x3000, 0x4000)
+    assert (a.q, a.k, a.v, a.o) == (0x1000, 0x2000, 0x3000, 0x4000)
+    assert a.seq_len == 100 and a.head_dim == 32 and a.causal == 1 and a.scale == 0.5
+    assert a.q_row_stride == 40 and a.k_row_stride == a.v_row_stride == a.o_row_stride == 32
+    assert a.num_q_blocks == -(-100 // sel.block_m) and a.batch_heads == 3
+    # the first 88 bytes are the reference kernels' parameter list (src/flash.zig:55-68)
+    assert nc.KernelArgs.scale.offset == 80 and nc.KernelArgs.causal.offset == 84
+
+
+def test_launch_validates_before_touching_the_module():
+    lib = nc.load_library()
+    bad = nc.options(batch_heads=1, seq_len=16, head_dim=24)
+    st = lib.nc_flash_launch(None, 0x1000, 10 ** 6, 0x1000, 10 ** 6, 0x1000, 10 ** 6, 0x1000, 10 ** 6,
+                             ctypes.byref(bad))
+    assert nc.STATUS_NAMES[st] == "InvalidValue"
+    good = nc.options(batch_heads=2, seq_len=16, head_dim=16)
+    # requireLen: one element short on O (src/flash.zig:43); fails before the (null) module is used
+    st = lib.nc_flash_launch(ctypes.c_void_p(0x10), 0x1000, 512, 0x1000, 512, 0x1000, 512, 0x1000, 511,
+                             ctypes.byref(good))
+    assert nc.STATUS_NAMES[st] == "InvalidValue"
+
+
+def test_work_model_matches_reference_formulas():
+    w = nc.work_model(CONFIGS["c3"].options())
+    assert w.flops_reference == 1_074_790_400  # BH*4*S(S+1)/2*d, src/main.zig:1032-1033
+    assert w.flops_halfsquare == 1_073_741_824  # 4*BH*S^2*d/2
+    assert w.bytes == 5_242_880  # BH*S*d*(3*2+4), src/main.zig:1034
+    w4 = nc.work_model(CONFIGS["c4"].options())
+    assert w4.flops_reference == w4.flops_halfsquare == 4 * 32 * 4096 * 4096 * 64
+
+
+def test_benchmark_arithmetic():
+    r = nc.benchmark_finish([1.0, 2.0, 3.0], bytes_=6_000_000, flops=4_000_000_000)
+    assert (r.mean_ms, r.min_ms, r.max_ms) == (2.0, 1.0, 3.0)
+    assert r.has_gbps and abs(r.throughput_gbps - 3.0) < 1e-6      # bytes/(mean_ms*1e6)
+    assert r.has_tflops and abs(r.tflops - 2.0) < 1e-6             # flops/(mean_ms*1e9)
+    r0 = nc.benchmark_finish([0.5])
+    assert not r0.has_gbps and not r0.has_tflops
+
+
+def test_bench_refuses_multi_gpu():
+    p = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert p.returncode == 2 and "one GPU" in p.stderr
+
+
+def test_f16_conversion_matches_numpy():
+    lib = nc.load_library()
+    h = np.arange(65536, dtype=np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    fin = np.isfinite(f)
+    back = np.array([lib.nc_f32_to_f16(float(x)) for x in f[fin][::5]], dtype=np.uint16)
+    assert np.array_equal(back, h[fin][::5])
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2 ** 32, size=20000, dtype=np.uint64).astype(np.uint32)
+    vals = bits.view(np.float32)
+    vals = vals[np.isfinite(vals)]
+    special = np.array([65504.0, 65519.99, 65520.0, 1e9, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -26,
+                        6.1e-5, 5.96e-8, -0.0, 0.0, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11], dtype=np.float32)
+    vals = np.concatenate([vals, special, -special])
+    got = np.array([lib.nc_f32_to_f16(float(x)) for x in vals], dtype=np.uint16)
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    assert lib.nc_f32_to_f16(float("inf")) == 0x7C00
+    assert (lib.nc_f32_to_f16(float("nan")) & 0x7C00) == 0x7C00 and (lib.nc_f32_to_f16(float("nan")) & 0x3FF)
+    dec = np.array([lib.nc_f16_to_f32(int(x)) for x in h[fin][::3]], dtype=np.float32)
+    assert np.array_equal(dec.view(np.uint32), f[fin][::3].view(np.uint32))
+
+
+def test_seeded_fills():
+    u = nc.fill_uniform(200_000, 1, 0, -1.0, 1.0).view(np.float16).astype(np.float64)
+    assert u.min() >= -1.0 and u.max() <= 1.0 and abs(u.mean()) < 0.01 and abs(u.std() - 1 / np.sqrt(3)) < 0.01
+    n = nc.fill_normal(200_001, 3, 1, 0.0, 3.0).view(np.float16).astype(np.float64)
+    assert abs(n.mean()) < 0.03 and abs(n.std() - 3.0) < 0.03
+    # deterministic, keyed by (seed, tensor), counter-based (prefixes agree)
+    assert np.array_equal(nc.fill_normal(1000, 3, 1), nc.fill_normal(1000, 3, 1))
+    assert np.array_equal(nc.fill_normal(1000, 3, 1), nc.fill_normal(5000, 3, 1)[:1000])
+    assert not np.array_equal(nc.fill_normal(1000, 3, 1), nc.fill_normal(1000, 3, 2))
+    assert not np.array_equal(nc.fill_uniform(1000, 3, 1), nc.fill_uniform(1000, 4, 1))
