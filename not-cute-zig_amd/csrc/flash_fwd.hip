@@ -35,6 +35,7 @@
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -373,11 +374,26 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
 #define NC_LDS(T) __attribute__((address_space(3))) T
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
+// LDS layout of a staged K or V block: row r (a key), 16-byte chunk ch (8 head columns) stored at
+// slot r*CH + (ch ^ f(r)). f is chosen for the two read patterns on gfx950's 64 x 4-byte banks:
+//  - K operand (ds_read_b128): 16 consecutive rows at one chunk must cover all sixteen 16-byte
+//    slots of a 256-byte bank window;
+//  - V^T operand (ds_read_b64_tr_b16): rows r..r+3 (r % 4 == 0) at four consecutive chunks must
+//    too, so for 128-byte rows f(r) and f(r+2) differ in bit 2.
 template <int D>
 struct Swz {
     static constexpr int CH = D / 8;  // 16-byte chunks per row
-    // slot of chunk ch in row r
-    __device__ static __forceinline__ int slot(int r, int ch) { return r * CH + (ch ^ ((r >> 1) & (CH - 1))); }
+    __device__ static __forceinline__ int f(int r) {
+        if constexpr (CH == 8) {
+            const int x = (r >> 1) & 7;
+            return ((x & 1) << 2) | (x >> 1);
+        } else if constexpr (CH == 4) {
+            return (r >> 2) & 3;
+        } else {
+            return (r >> 3) & 1;
+        }
+    }
+    __device__ static __forceinline__ int slot(int r, int ch) { return r * CH + (ch ^ f(r)); }
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
@@ -427,6 +443,25 @@ __device__ __forceinline__ void wait_lds_tied(u32x2 (&v)[MT][2][2]) {
                      : "+v"(v[0][0][0]), "+v"(v[0][0][1]), "+v"(v[0][1][0]), "+v"(v[0][1][1]),
                        "+v"(v[1][0][0]), "+v"(v[1][0][1]), "+v"(v[1][1][0]), "+v"(v[1][1][1]));
     }
+}
+
+template <int N>
+struct IC {
+    static constexpr int value = N;
+};
+
+// LDS reads at a lane address plus a compile-time byte offset (folded into the instruction's
+// 16-bit offset field when it fits).
+template <int OFF>
+__device__ __forceinline__ half8 lds_load_b128(uint32_t addr) {
+    return *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(addr + (uint32_t)OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void ds_read_tr(u32x2 &out, uint32_t addr) {
+    if constexpr (OFF < 65536)
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(out) : "v"(addr), "i"(OFF));
+    else
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(out) : "v"(addr + (uint32_t)OFF));
 }
 
 template <int D, int NQ, int NS, int NSTAGE>
@@ -504,15 +539,14 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         qf[kk] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
                                                qr, (uint32_t)qrow * qrb + (16 * kk + 8 * hh) * 2, 0, 0));
 
-    if (tid < 4) reinterpret_cast<uint32_t *>(smem + C::ZERO_OFF)[tid] = 0u;
-
     const int kv_end = CAUSAL ? min(S, q0 + C::BM) : S;
     const int nblk = (kv_end + C::BN - 1) / C::BN;
 
-    // Per-lane constant parts of the staging addresses: wave-instruction t of a block covers
-    // 16-byte slots [64t, 64t+64) of the K tile (t < LOADS/2) or of the V tile.
-    auto issue = [&](int blk) {
-        char *sbase = smem + (blk % NSTAGE) * C::STAGE;
+    // Staging: wave-instruction t of a block fills 16-byte slots [64t, 64t+64) of the K tile
+    // (t < LOADS/2) or of the V tile; the ring stage is a compile-time constant.
+    auto issue = [&](int blk, auto stage_c) {
+        constexpr int ST = decltype(stage_c)::value;
+        char *sbase = smem + ST * C::STAGE;
 #pragma unroll
         for (int n = 0; n < C::LPW; ++n) {
             const int t = w + C::NW * n;
@@ -520,7 +554,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             const int tt = isv ? t - C::LOADS / 2 : t;
             const int p = tt * 64 + lane;
             const int r = p / C::CH, sl = p % C::CH;
-            const int ch = sl ^ ((r >> 1) & (C::CH - 1));
+            const int ch = sl ^ SW::f(r);
             const uint32_t key = (uint32_t)(blk * C::BN + r);
             NC_LDS(void) *dst = (NC_LDS(void) *)(sbase + (isv ? C::TILE : 0) + tt * 1024);
             if (isv)
@@ -530,26 +564,26 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
     };
 
-    // Lane-constant LDS byte offsets of the MFMA operand reads inside a stage.
+    // Lane-dependent LDS byte offsets of the MFMA operand reads within stage 0; stages, and the
+    // second 16-key half of a sub-tile, add compile-time offsets (the swizzle is periodic in 16 rows).
     //  K (A operand of S^T): row 32s + c, chunk 2kk + hh.
-    int koff[D / 16];
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+    uint32_t kaddr[D / 16];
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) koff[kk] = SW::slot(32 * s + c, 2 * kk + hh) * 16;
-    //  V^T (A operand of O^T), per (mt, ks, hf): rows 32s + 16ks + 8hf + 4*hv + m/4, columns
-    //  32mt + 16cg + 4(m%4) .. +3, where the 16-lane group index is G = 2*hv + cg.
-    const int G = lane >> 4, m = lane & 15, hv = G >> 1, cg = G & 1;
-    int voff[C::MT][2][2];
+    for (int kk = 0; kk < D / 16; ++kk) kaddr[kk] = lds0 + SW::slot(32 * s + c, 2 * kk + hh) * 16;
+    //  V^T (A operand of O^T), per (mt, hf): rows 32s + 8hf + 4*hv + m/4 (+16 for the second key
+    //  step), columns 32mt + 16cg + 4(m%4) .. +3, with 16-lane group G = 2*hv + cg. Head 16 pads
+    //  O^T to 32 rows: its lanes for columns 16..31 re-read columns 0..15 (those rows are dropped).
+    const int G = lane >> 4, m = lane & 15, hv = G >> 1, cg = D < 32 ? 0 : (G & 1);
+    uint32_t vaddr[C::MT][2];
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const int r = 32 * s + 16 * ks + 8 * hf + 4 * hv + (m >> 2);
-                const int d = 32 * mt + 16 * cg + 4 * (m & 3);
-                voff[mt][ks][hf] = (d < D) ? C::TILE + SW::slot(r, d >> 3) * 16 + ((d >> 2) & 1) * 8
-                                           : -1;  // head 16: columns 16..31 of the padded tile are zero
-            }
+        for (int hf = 0; hf < 2; ++hf) {
+            const int r = 32 * s + 8 * hf + 4 * hv + (m >> 2);
+            const int d = 32 * mt + 16 * cg + 4 * (m & 3);
+            vaddr[mt][hf] = lds0 + C::TILE + SW::slot(r, d >> 3) * 16 + ((d >> 2) & 1) * 8;
+        }
 
     // Log2-domain scale. A negative scale is applied by negating the resident Q operand (exact),
     // a zero scale by a tiny positive one (every score then rounds to weight exp2(0) = 1, as with
@@ -567,25 +601,23 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt) o[mt] = floatx16{};
 
-#pragma unroll
-    for (int b = 0; b < NSTAGE - 1; ++b)
-        if (b < nblk) issue(b);
-
-    for (int blk = 0; blk < nblk; ++blk) {
+    // One key block: wait for its stage, refill the stage consumed last step, compute this wave's
+    // 32x32 sub-tile.
+    auto step = [&](int blk, auto stage_c) {
+        constexpr int ST = decltype(stage_c)::value;
         wait_block<C::LPW, NSTAGE>(min(NSTAGE - 2, nblk - 1 - blk));
-        if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1);
+        if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
 
         const int kt0 = blk * C::BN + 32 * s;
         bool run = kt0 < S;
         if (CAUSAL) run = run && kt0 <= qw_last;
-        if (!run) continue;
+        if (!run) return;
 
-        const char *st = smem + (blk % NSTAGE) * C::STAGE;
         floatx16 acc = floatx16{};
         half8 kf[D / 16];
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
-            kf[kk] = *reinterpret_cast<const half8 *>(st + koff[kk]);
+            kf[kk] = lds_load_b128<ST * C::STAGE>(kaddr[kk]);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], acc, 0, 0, 0);
         }
         lds_reads_done<D / 16>(kf);
@@ -596,15 +628,12 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         // wait_lds_tied() waits for these reads and ties the registers to that wait.
         u32x2 vt[C::MT][2][2];
 #pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const int off = voff[mt][ks][hf];
-                    const uint32_t addr = (uint32_t)(uintptr_t)(off >= 0 ? st + off : smem + C::ZERO_OFF);
-                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(vt[mt][ks][hf]) : "v"(addr));
-                }
+        for (int mt = 0; mt < C::MT; ++mt) {
+            ds_read_tr<ST * C::STAGE>(vt[mt][0][0], vaddr[mt][0]);
+            ds_read_tr<ST * C::STAGE>(vt[mt][0][1], vaddr[mt][1]);
+            ds_read_tr<ST * C::STAGE + 16 * C::CH * 16>(vt[mt][1][0], vaddr[mt][0]);
+            ds_read_tr<ST * C::STAGE + 16 * C::CH * 16>(vt[mt][1][1], vaddr[mt][1]);
+        }
 
         // Online softmax on raw scores (sc > 0): the tile max is taken before scaling, which is
         // exact because rounding is monotonic, and scale + subtract fuse into one FMA. The running
@@ -617,10 +646,10 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             for (int r = 0; r < 16; ++r)
                 if (8 * (r >> 2) + 4 * hh + (r & 3) > lim) acc[r] = neg_inf();
         }
-        float tmax = fmaxf(fmaxf(acc[0], acc[1]), acc[2]);
-#pragma unroll
-        for (int r = 3; r < 15; r += 2) tmax = fmaxf(fmaxf(tmax, acc[r]), acc[r + 1]);
-        tmax = fmaxf(tmax, acc[15]);
+        const float m0 = fmaxf(fmaxf(acc[0], acc[1]), acc[2]), m1 = fmaxf(fmaxf(acc[3], acc[4]), acc[5]);
+        const float m2 = fmaxf(fmaxf(acc[6], acc[7]), acc[8]), m3 = fmaxf(fmaxf(acc[9], acc[10]), acc[11]);
+        const float m4 = fmaxf(fmaxf(acc[12], acc[13]), acc[14]);
+        const float tmax = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), acc[15]));
         const float m_tile = pair_max(tmax) * sc;
         if (__builtin_amdgcn_ballot_w64(m_tile > mrow + kRescaleLog2)) {
             const float m_new = fmaxf(mrow, m_tile);
@@ -631,20 +660,19 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             mrow = m_new;
         }
         const float neg_m = (mrow == neg_inf()) ? 0.f : -mrow;
-        float p[16];
-        float psum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], sc, neg_m));
-            psum += p[r];
-        }
-        l += psum;
-
         half8 pf[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], sc, neg_m));
+        // Row sum of the weights as rounded for the PV product (v_dot2c against 1.0 pairs); the
+        // numerator and the denominator then use the same P.
+        const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) pf[ks][j] = (_Float16)p[8 * ks + j];
+            for (int j = 0; j < 4; ++j) {
+                const half2v h = {pf[ks][2 * j], pf[ks][2 * j + 1]};
+                l = __builtin_amdgcn_fdot2(h, ones, l, false);
+            }
 
         wait_lds_tied<C::MT>(vt);
 #pragma unroll
@@ -654,6 +682,20 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 const u32x4 vv = {vt[mt][ks][0][0], vt[mt][ks][0][1], vt[mt][ks][1][0], vt[mt][ks][1][1]};
                 o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, vv), pf[ks], o[mt], 0, 0, 0);
             }
+    };
+
+    issue(0, IC<0>{});
+    if constexpr (NSTAGE > 2)
+        if (1 < nblk) issue(1, IC<1>{});
+    if constexpr (NSTAGE > 3)
+        if (2 < nblk) issue(2, IC<2>{});
+    for (int blk0 = 0; blk0 < nblk; blk0 += NSTAGE) {
+        step(blk0, IC<0>{});
+        if (blk0 + 1 < nblk) step(blk0 + 1, IC<1>{});
+        if constexpr (NSTAGE > 2)
+            if (blk0 + 2 < nblk) step(blk0 + 2, IC<2>{});
+        if constexpr (NSTAGE > 3)
+            if (blk0 + 3 < nblk) step(blk0 + 3, IC<3>{});
     }
 
     // Epilogue (all loads landed, all LDS reads done), as in flash_fwd_body.
@@ -699,7 +741,8 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             const floatx4 oj = *reinterpret_cast<const floatx4 *>(ob + (base + 32 * j) * C::OP + 4 * ch);
             accv += wgt * oj;
         }
-        floatx4 res = {accv[0] / den, accv[1] / den, accv[2] / den, accv[3] / den};
+        const float inv = 1.f / den;
+        floatx4 res = accv * inv;
         *reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch) = res;
     }
 }
