@@ -29,19 +29,20 @@ struct Variant {
     uint32_t nq;      // query waves (32 rows each)
     uint32_t ns;      // key-split waves
     uint32_t nstage;  // LDS ring depth (pipelined family)
+    uint32_t sub;     // 32-key sub-tiles per wave per block (pipelined family)
     bool causal;
     bool aligned;
     Family family;
 
     uint32_t bm() const { return 32 * nq; }
-    uint32_t bn() const { return 32 * ns; }
+    uint32_t bn() const { return 32 * ns * sub; }
     uint32_t threads() const { return 64 * nq * ns; }
     uint32_t lds_bytes() const {
         const uint32_t nw = nq * ns;
         const uint32_t o_bytes = nw * 32 * (d + 4) * 4;
         if (family == Family::kPipe) {
             const uint32_t ring = nstage * 2 * bn() * d * 2;
-            return (ring > o_bytes ? ring : o_bytes) + 16 + nw * 32 * 2 * 4;
+            return (ring > o_bytes ? ring : o_bytes) + nw * 32 * 2 * 4;
         }
         const uint32_t dv = d < 32 ? 32 : d;
         const uint32_t stage = bn() * (d + 8) * 2 + dv * (bn() + 8) * 2;
@@ -49,9 +50,9 @@ struct Variant {
     }
 };
 
-#define PIPE(D, NQ, NS, P, C) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "_" C, D, NQ, NS, P, \
+#define PIPE(D, NQ, NS, P, C) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "_" C, D, NQ, NS, P, 1, \
                                C[0] == 'c', true, Family::kPipe}
-#define GEN(D, C, A, SUF) {"nc_flash_fwd_d" #D "_m64_" C SUF, D, 2, 2, 1, C[0] == 'c', A, Family::kGeneric}
+#define GEN(D, C, A, SUF) {"nc_flash_fwd_d" #D "_m64_" C SUF, D, 2, 2, 1, 1, C[0] == 'c', A, Family::kGeneric}
 
 const Variant kVariants[] = {
     PIPE(64, 8, 1, 3, "full"), PIPE(64, 8, 1, 3, "causal"), PIPE(64, 4, 1, 3, "full"), PIPE(64, 4, 1, 3, "causal"),
@@ -70,7 +71,8 @@ const Variant kVariants[] = {
 
 const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal) {
     for (const auto &v : kVariants)
-        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.causal == causal) return &v;
+        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.sub == 1 && v.causal == causal)
+            return &v;
     return nullptr;
 }
 

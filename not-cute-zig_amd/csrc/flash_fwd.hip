@@ -38,6 +38,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -410,6 +411,26 @@ __device__ __forceinline__ void wait_vm_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
+// s_waitcnt vmcnt(N) only (no barrier): the wave's own staged loads of the block it is about to
+// use have landed in LDS, and its earlier LDS reads are complete (lgkmcnt(0)).
+template <int N>
+__device__ __forceinline__ void wait_vm_only() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");
+}
+
+template <int LPW, int NSTAGE>
+__device__ __forceinline__ void wait_vm_own(int ahead) {
+    if constexpr (NSTAGE >= 4) {
+        if (ahead >= 2) { wait_vm_only<2 * LPW>(); return; }
+    }
+    if constexpr (NSTAGE >= 3) {
+        if (ahead >= 1) { wait_vm_only<LPW>(); return; }
+    }
+    wait_vm_only<0>();
+}
+
 template <int LPW, int NSTAGE>
 __device__ __forceinline__ void wait_block(int ahead) {
     // ahead = blocks issued after the one about to be consumed (0 .. NSTAGE-2)
@@ -426,29 +447,40 @@ __device__ __forceinline__ void wait_block(int ahead) {
 // been waited for, so asm-issued LDS reads that follow never sit under a compiler lgkmcnt wait.
 template <int N>
 __device__ __forceinline__ void lds_reads_done(half8 (&k)[N]) {
-    if constexpr (N == 1) asm volatile("" ::"v"(k[0]));
-    else if constexpr (N == 2) asm volatile("" ::"v"(k[0]), "v"(k[1]));
-    else asm volatile("" ::"v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]));
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+        if constexpr (N % 4 != 0) {
+            asm volatile("" ::"v"(k[i]));
+        } else {
+            asm volatile("" ::"v"(k[i]), "v"(k[i + 1]), "v"(k[i + 2]), "v"(k[i + 3]));
+        }
+    }
 }
 
 // s_waitcnt lgkmcnt(0) that the compiler sees as producing the given registers, so no consumer of
-// an asm-issued LDS read can be scheduled before the wait.
-template <int MT>
-__device__ __forceinline__ void wait_lds_tied(u32x2 (&v)[MT][2][2]) {
-    if constexpr (MT == 1) {
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0][0][0]), "+v"(v[0][0][1]), "+v"(v[0][1][0]), "+v"(v[0][1][1]));
-    } else {
-        static_assert(MT == 2, "head 64 at most");
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(v[0][0][0]), "+v"(v[0][0][1]), "+v"(v[0][1][0]), "+v"(v[0][1][1]),
-                       "+v"(v[1][0][0]), "+v"(v[1][0][1]), "+v"(v[1][1][0]), "+v"(v[1][1][1]));
-    }
+// an asm-issued LDS read can be scheduled before the wait. Registers beyond the first four are
+// tied by empty asm statements that follow the wait (asm volatile statements keep their order).
+template <int N>
+__device__ __forceinline__ void wait_lds_tied(u32x2 (&v)[N]) {
+    static_assert(N % 4 == 0, "groups of four");
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+#pragma unroll
+    for (int i = 4; i < N; i += 4) asm volatile("" : "+v"(v[i]), "+v"(v[i + 1]), "+v"(v[i + 2]), "+v"(v[i + 3]));
 }
 
 template <int N>
 struct IC {
     static constexpr int value = N;
 };
+
+// Calls f(IC<I>{}) for I = B .. E-1 (compile-time loop index).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(IC<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
 
 // LDS reads at a lane address plus a compile-time byte offset (folded into the instruction's
 // 16-bit offset field when it fits).
@@ -464,32 +496,33 @@ __device__ __forceinline__ void ds_read_tr(u32x2 &out, uint32_t addr) {
         asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(out) : "v"(addr + (uint32_t)OFF));
 }
 
-template <int D, int NQ, int NS, int NSTAGE>
+template <int D, int NQ, int NS, int NSTAGE, int SUB>
 struct PipeCfg {
     static constexpr int NW = NQ * NS;
     static constexpr int NT = NW * 64;
     static constexpr int BM = 32 * NQ;
-    static constexpr int BN = 32 * NS;
+    static constexpr int WK = 32 * SUB;                 // keys per wave per block
+    static constexpr int BN = WK * NS;                  // keys staged per block
     static constexpr int CH = D / 8;
     static constexpr int TILE = BN * D * 2;             // bytes of one K (or V) block
     static constexpr int STAGE = 2 * TILE;
     static constexpr int LOADS = 2 * BN * CH / 64;      // wave-level 16-byte load instructions per block
     static_assert(LOADS % NW == 0, "every wave issues the same number of loads per block");
     static constexpr int LPW = LOADS / NW;
+    static_assert(NQ != 1 || LPW % 2 == 0, "private staging: each wave loads as many K as V rows");
     static constexpr int RING = NSTAGE * STAGE;
     static constexpr int OP = D + 4;
     static constexpr int O_BYTES = NW * 32 * OP * 4;
-    static constexpr int ZERO_OFF = RING > O_BYTES ? RING : O_BYTES;
-    static constexpr int ML_OFF = ZERO_OFF + 16;
+    static constexpr int ML_OFF = RING > O_BYTES ? RING : O_BYTES;
     static constexpr int LDS_BYTES = ML_OFF + NW * 32 * 2 * 4;
     static constexpr int MT = D < 32 ? 1 : D / 32;
 };
 
-template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE>
+template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB>
 __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &a) {
-    using C = PipeCfg<D, NQ, NS, NSTAGE>;
+    using C = PipeCfg<D, NQ, NS, NSTAGE, SUB>;
     using SW = Swz<D>;
-    static_assert(NSTAGE >= 2 && NSTAGE <= 4, "ring depth");
+    static_assert(NSTAGE >= 1 && NSTAGE <= 4, "ring depth");
     __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
 
     if (a.head_dim != (uint64_t)D || a.seq_len == 0) return;
@@ -539,8 +572,16 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         qf[kk] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
                                                qr, (uint32_t)qrow * qrb + (16 * kk + 8 * hh) * 2, 0, 0));
 
+    // One query group per workgroup: every wave consumes only its own key slice of each block,
+    // so each wave stages that slice itself and no barrier is needed until the epilogue; a wave
+    // runs only over the blocks where its slice has visible keys.
+    constexpr bool PRIV = (NQ == 1);
     const int kv_end = CAUSAL ? min(S, q0 + C::BM) : S;
-    const int nblk = (kv_end + C::BN - 1) / C::BN;
+    int nblk = (kv_end + C::BN - 1) / C::BN;
+    if constexpr (PRIV) {
+        const int last_key = (CAUSAL ? min(S - 1, qw_last) : S - 1) - C::WK * s;
+        nblk = last_key < 0 ? 0 : last_key / C::BN + 1;
+    }
 
     // Staging: wave-instruction t of a block fills 16-byte slots [64t, 64t+64) of the K tile
     // (t < LOADS/2) or of the V tile; the ring stage is a compile-time constant.
@@ -549,7 +590,10 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         char *sbase = smem + ST * C::STAGE;
 #pragma unroll
         for (int n = 0; n < C::LPW; ++n) {
-            const int t = w + C::NW * n;
+            // Shared staging: wave-instructions are dealt round-robin over the waves. Private
+            // staging (one query group): wave s loads exactly the rows of its own key slice.
+            const int t = PRIV ? (n < C::LPW / 2 ? s * (C::LPW / 2) + n : C::LOADS / 2 + s * (C::LPW / 2) + n - C::LPW / 2)
+                               : w + C::NW * n;
             const bool isv = t >= C::LOADS / 2;
             const int tt = isv ? t - C::LOADS / 2 : t;
             const int p = tt * 64 + lane;
@@ -564,26 +608,28 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
     };
 
-    // Lane-dependent LDS byte offsets of the MFMA operand reads within stage 0; stages, and the
-    // second 16-key half of a sub-tile, add compile-time offsets (the swizzle is periodic in 16 rows).
-    //  K (A operand of S^T): row 32s + c, chunk 2kk + hh.
+    // Lane-dependent LDS byte offsets of the MFMA operand reads within stage 0; stages, sub-tiles
+    // and the second 16-key half of a sub-tile add compile-time offsets (the swizzle repeats every
+    // 16 rows).
+    //  K (A operand of S^T): row WK*s + 32j + c, chunk 2kk + hh.
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
     uint32_t kaddr[D / 16];
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) kaddr[kk] = lds0 + SW::slot(32 * s + c, 2 * kk + hh) * 16;
-    //  V^T (A operand of O^T), per (mt, hf): rows 32s + 8hf + 4*hv + m/4 (+16 for the second key
-    //  step), columns 32mt + 16cg + 4(m%4) .. +3, with 16-lane group G = 2*hv + cg. Head 16 pads
-    //  O^T to 32 rows: its lanes for columns 16..31 re-read columns 0..15 (those rows are dropped).
+    for (int kk = 0; kk < D / 16; ++kk) kaddr[kk] = lds0 + SW::slot(C::WK * s + c, 2 * kk + hh) * 16;
+    //  V^T (A operand of O^T), per (mt, hf): rows WK*s + 32j + 16ks + 8hf + 4*hv + m/4, columns
+    //  32mt + 16cg + 4(m%4) .. +3, with 16-lane group G = 2*hv + cg. Head 16 pads O^T to 32 rows:
+    //  its lanes for columns 16..31 re-read columns 0..15 (those output rows are dropped).
     const int G = lane >> 4, m = lane & 15, hv = G >> 1, cg = D < 32 ? 0 : (G & 1);
     uint32_t vaddr[C::MT][2];
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-            const int r = 32 * s + 8 * hf + 4 * hv + (m >> 2);
+            const int r = C::WK * s + 8 * hf + 4 * hv + (m >> 2);
             const int d = 32 * mt + 16 * cg + 4 * (m & 3);
             vaddr[mt][hf] = lds0 + C::TILE + SW::slot(r, d >> 3) * 16 + ((d >> 2) & 1) * 8;
         }
+    constexpr int ROW16 = 16 * C::CH * 16;  // bytes of 16 staged rows
 
     // Log2-domain scale. A negative scale is applied by negating the resident Q operand (exact),
     // a zero scale by a tiny positive one (every score then rounds to weight exp2(0) = 1, as with
@@ -605,51 +651,88 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // 32x32 sub-tile.
     auto step = [&](int blk, auto stage_c) {
         constexpr int ST = decltype(stage_c)::value;
-        wait_block<C::LPW, NSTAGE>(min(NSTAGE - 2, nblk - 1 - blk));
-        if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
+        if constexpr (PRIV && NSTAGE == 1) {
+            // Private single stage: the wave's reads of the previous block are complete (their
+            // results were consumed), so it refills the stage with this block and waits for it.
+            if (blk > 0) issue(blk, IC<0>{});
+            wait_vm_only<0>();
+        } else if constexpr (PRIV) {
+            wait_vm_own<C::LPW, NSTAGE>(min(NSTAGE - 2, nblk - 1 - blk));
+            if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
+        } else if constexpr (NSTAGE == 1) {
+            // Single stage: refill it once every wave is done with the previous block.
+            if (blk > 0) {
+                __builtin_amdgcn_s_waitcnt(0xc07f & ~(0xf << 8));  // lgkmcnt(0)
+                asm volatile("s_barrier" ::: "memory");
+                issue(blk, IC<0>{});
+            }
+            wait_vm_barrier<0>();
+        } else {
+            wait_block<C::LPW, NSTAGE>(min(NSTAGE - 2, nblk - 1 - blk));
+            if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
+        }
 
-        const int kt0 = blk * C::BN + 32 * s;
+        const int kt0 = blk * C::BN + C::WK * s;  // this wave's first key
         bool run = kt0 < S;
         if (CAUSAL) run = run && kt0 <= qw_last;
         if (!run) return;
 
-        floatx16 acc = floatx16{};
-        half8 kf[D / 16];
+        // S^T for SUB consecutive 32-key sub-tiles (independent MFMA chains).
+        floatx16 acc[SUB];
+        half8 kf[SUB * (D / 16)];
+        static_for<0, SUB>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            acc[j] = floatx16{};
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-            kf[kk] = lds_load_b128<ST * C::STAGE>(kaddr[kk]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], acc, 0, 0, 0);
-        }
-        lds_reads_done<D / 16>(kf);
-        // V^T operands, issued once every K read of this sub-tile has landed (lds_reads_done
-        // orders them) so their latency hides behind the softmax. ds_read_b64_tr_b16 goes
-        // through asm: the builtin is treated as aliasing the in-flight buffer->LDS loads of later
-        // blocks, and the compiler would drain them (vmcnt(0)) before every read.
-        // wait_lds_tied() waits for these reads and ties the registers to that wait.
-        u32x2 vt[C::MT][2][2];
+            for (int kk = 0; kk < D / 16; ++kk) {
+                kf[j * (D / 16) + kk] = lds_load_b128<ST * C::STAGE + 2 * j * ROW16>(kaddr[kk]);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[j * (D / 16) + kk], qf[kk], acc[j], 0, 0, 0);
+            }
+        });
+        lds_reads_done(kf);
+        // V^T operands, issued once every K read of this step has landed (lds_reads_done orders
+        // them) so their latency hides behind the softmax. ds_read_b64_tr_b16 goes through asm:
+        // the builtin is treated as aliasing the in-flight buffer->LDS loads of later blocks, and
+        // the compiler would drain them (vmcnt(0)) before every read. wait_lds_tied() waits for
+        // these reads and ties the registers to that wait.
+        u32x2 vt[SUB * C::MT * 4];
+        static_for<0, SUB>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
 #pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt) {
-            ds_read_tr<ST * C::STAGE>(vt[mt][0][0], vaddr[mt][0]);
-            ds_read_tr<ST * C::STAGE>(vt[mt][0][1], vaddr[mt][1]);
-            ds_read_tr<ST * C::STAGE + 16 * C::CH * 16>(vt[mt][1][0], vaddr[mt][0]);
-            ds_read_tr<ST * C::STAGE + 16 * C::CH * 16>(vt[mt][1][1], vaddr[mt][1]);
-        }
+            for (int mt = 0; mt < C::MT; ++mt) {
+                u32x2 *v4 = vt + (j * C::MT + mt) * 4;
+                ds_read_tr<ST * C::STAGE + 2 * j * ROW16>(v4[0], vaddr[mt][0]);
+                ds_read_tr<ST * C::STAGE + 2 * j * ROW16>(v4[1], vaddr[mt][1]);
+                ds_read_tr<ST * C::STAGE + 2 * j * ROW16 + ROW16>(v4[2], vaddr[mt][0]);
+                ds_read_tr<ST * C::STAGE + 2 * j * ROW16 + ROW16>(v4[3], vaddr[mt][1]);
+            }
+        });
 
-        // Online softmax on raw scores (sc > 0): the tile max is taken before scaling, which is
-        // exact because rounding is monotonic, and scale + subtract fuse into one FMA. The running
-        // max only moves (and O, l are rescaled) when some lane's max grows by more than 2^8, so P
+        // Online softmax on raw scores (sc > 0): the max is taken before scaling, which is exact
+        // because rounding is monotonic, and scale + subtract fuse into one FMA. The running max
+        // only moves (and O, l are rescaled) when some lane's max grows by more than 2^8, so P
         // stays <= 256 (exact in f16 range) and the 32-multiply O rescale is rare.
-        const bool need_mask = (kt0 + 32 > S) || (CAUSAL && kt0 + 31 > qw0);
+        const bool need_mask = (kt0 + C::WK > S) || (CAUSAL && kt0 + C::WK - 1 > qw0);
         if (need_mask) {
             const int lim = CAUSAL ? min(qrow, S - 1) - kt0 : S - 1 - kt0;  // last visible key offset
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (8 * (r >> 2) + 4 * hh + (r & 3) > lim) acc[r] = neg_inf();
+            for (int j = 0; j < SUB; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (32 * j + 8 * (r >> 2) + 4 * hh + (r & 3) > lim) acc[j][r] = neg_inf();
         }
-        const float m0 = fmaxf(fmaxf(acc[0], acc[1]), acc[2]), m1 = fmaxf(fmaxf(acc[3], acc[4]), acc[5]);
-        const float m2 = fmaxf(fmaxf(acc[6], acc[7]), acc[8]), m3 = fmaxf(fmaxf(acc[9], acc[10]), acc[11]);
-        const float m4 = fmaxf(fmaxf(acc[12], acc[13]), acc[14]);
-        const float tmax = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), acc[15]));
+        float mj[SUB];
+#pragma unroll
+        for (int j = 0; j < SUB; ++j) {
+            const floatx16 &x = acc[j];
+            const float m0 = fmaxf(fmaxf(x[0], x[1]), x[2]), m1 = fmaxf(fmaxf(x[3], x[4]), x[5]);
+            const float m2 = fmaxf(fmaxf(x[6], x[7]), x[8]), m3 = fmaxf(fmaxf(x[9], x[10]), x[11]);
+            const float m4 = fmaxf(fmaxf(x[12], x[13]), x[14]);
+            mj[j] = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), x[15]));
+        }
+        float tmax = mj[0];
+#pragma unroll
+        for (int j = 1; j < SUB; ++j) tmax = fmaxf(tmax, mj[j]);
         const float m_tile = pair_max(tmax) * sc;
         if (__builtin_amdgcn_ballot_w64(m_tile > mrow + kRescaleLog2)) {
             const float m_new = fmaxf(mrow, m_tile);
@@ -660,50 +743,81 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             mrow = m_new;
         }
         const float neg_m = (mrow == neg_inf()) ? 0.f : -mrow;
-        half8 pf[2];
+        half8 pf[SUB][2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], sc, neg_m));
+        for (int j = 0; j < SUB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                pf[j][r >> 3][r & 7] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][r], sc, neg_m));
         // Row sum of the weights as rounded for the PV product (v_dot2c against 1.0 pairs); the
         // numerator and the denominator then use the same P.
         const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int j = 0; j < SUB; ++j)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const half2v h = {pf[ks][2 * j], pf[ks][2 * j + 1]};
-                l = __builtin_amdgcn_fdot2(h, ones, l, false);
-            }
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const half2v h = {pf[j][ks][2 * t], pf[j][ks][2 * t + 1]};
+                    l = __builtin_amdgcn_fdot2(h, ones, l, false);
+                }
 
-        wait_lds_tied<C::MT>(vt);
+        wait_lds_tied(vt);
 #pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt)
+        for (int j = 0; j < SUB; ++j)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const u32x4 vv = {vt[mt][ks][0][0], vt[mt][ks][0][1], vt[mt][ks][1][0], vt[mt][ks][1][1]};
-                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, vv), pf[ks], o[mt], 0, 0, 0);
-            }
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const u32x2 *v4 = vt + (j * C::MT + mt) * 4 + 2 * ks;
+                    const u32x4 vv = {v4[0][0], v4[0][1], v4[1][0], v4[1][1]};
+                    o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, vv), pf[j][ks], o[mt], 0, 0, 0);
+                }
     };
 
-    issue(0, IC<0>{});
+    if (nblk > 0) issue(0, IC<0>{});
     if constexpr (NSTAGE > 2)
         if (1 < nblk) issue(1, IC<1>{});
     if constexpr (NSTAGE > 3)
         if (2 < nblk) issue(2, IC<2>{});
     for (int blk0 = 0; blk0 < nblk; blk0 += NSTAGE) {
         step(blk0, IC<0>{});
-        if (blk0 + 1 < nblk) step(blk0 + 1, IC<1>{});
+        if constexpr (NSTAGE > 1)
+            if (blk0 + 1 < nblk) step(blk0 + 1, IC<1>{});
         if constexpr (NSTAGE > 2)
             if (blk0 + 2 < nblk) step(blk0 + 2, IC<2>{});
         if constexpr (NSTAGE > 3)
             if (blk0 + 3 < nblk) step(blk0 + 3, IC<3>{});
     }
 
-    // Epilogue (all loads landed, all LDS reads done), as in flash_fwd_body.
-    wait_vm_barrier<0>();
-    float *ob = reinterpret_cast<float *>(smem);
-    float *mb = reinterpret_cast<float *>(smem + C::ML_OFF);
-    float *lb = mb + C::NW * 32;
+    // Epilogue. (1) Each wave publishes its per-query (m, l) in a dedicated LDS area (no wave
+    // reads the staging ring any more once it is past its loop, but others may still be in theirs,
+    // so the ring is not touched yet). (2) After one barrier every lane derives, for its query, the
+    // merge weight exp2(m_s - M) / L of its own partial (M = max over the NS key splits,
+    // L = sum exp2(m_j - M) l_j), scales its O^T partial in registers and writes it over the ring.
+    // (3) After a second barrier each output float4 is the plain sum of NS scaled partials, stored
+    // row-contiguously (coalesced).
+    float2v *mlb = reinterpret_cast<float2v *>(smem + C::ML_OFF);  // [BM queries][NS splits]
     const float lt = pair_sum(l);
+    if (hh == 0) mlb[(qg * 32 + c) * NS + s] = float2v{mrow, lt};
+    wait_vm_barrier<0>();
+    float scale_own;
+    if constexpr (NS == 1) {
+        scale_own = 1.f / lt;
+    } else {
+        const float2v *row = mlb + (qg * 32 + c) * NS;
+        float2v ml[NS];
+#pragma unroll
+        for (int j = 0; j < NS; ++j) ml[j] = row[j];
+        float mmax = ml[0][0];
+#pragma unroll
+        for (int j = 1; j < NS; ++j) mmax = fmaxf(mmax, ml[j][0]);
+        float den = 0.f;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) den += __builtin_amdgcn_exp2f(ml[j][0] - mmax) * ml[j][1];
+        scale_own = __builtin_amdgcn_exp2f(mrow - mmax) / den;  // exp2(-inf) = 0 for empty splits
+    }
+    float *ob = reinterpret_cast<float *>(smem);
     {
         float *dst = ob + (w * 32 + c) * C::OP;
 #pragma unroll
@@ -713,13 +827,9 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 const int d = 32 * mt + 8 * i + 4 * hh;
                 if (d < D) {
                     floatx4 t = {o[mt][4 * i], o[mt][4 * i + 1], o[mt][4 * i + 2], o[mt][4 * i + 3]};
-                    *reinterpret_cast<floatx4 *>(dst + d) = t;
+                    *reinterpret_cast<floatx4 *>(dst + d) = t * scale_own;
                 }
             }
-        if (hh == 0) {
-            mb[w * 32 + c] = mrow;
-            lb[w * 32 + c] = lt;
-        }
     }
     __syncthreads();
     constexpr int DC = D / 4;
@@ -727,23 +837,11 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         const int qi = u / DC, ch = u % DC;
         const int row = q0 + qi;
         if (row >= S) continue;
-        const int base = (qi / 32) * NS * 32 + (qi % 32);
-        float ms = neg_inf();
+        const float *src = ob + ((qi / 32) * NS * 32 + (qi % 32)) * C::OP + 4 * ch;
+        floatx4 res = *reinterpret_cast<const floatx4 *>(src);
 #pragma unroll
-        for (int j = 0; j < NS; ++j) ms = fmaxf(ms, mb[base + 32 * j]);
-        floatx4 accv = {0.f, 0.f, 0.f, 0.f};
-        float den = 0.f;
-#pragma unroll
-        for (int j = 0; j < NS; ++j) {
-            const float mj = mb[base + 32 * j];
-            const float wgt = (NS == 1) ? 1.f : __builtin_amdgcn_exp2f(mj - ms);
-            den += wgt * lb[base + 32 * j];
-            const floatx4 oj = *reinterpret_cast<const floatx4 *>(ob + (base + 32 * j) * C::OP + 4 * ch);
-            accv += wgt * oj;
-        }
-        const float inv = 1.f / den;
-        floatx4 res = accv * inv;
-        *reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch) = res;
+        for (int j = 1; j < NS; ++j) res += *reinterpret_cast<const floatx4 *>(src + 32 * j * C::OP);
+        __builtin_nontemporal_store(res, reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch));
     }
 }
 
@@ -777,27 +875,28 @@ extern "C" __global__ __launch_bounds__(256) void nc_util_copy_b128(const u32x4 
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256ull) dst[i] = src[i];
 }
 
-#define NC_FLASH_PIPE_KERNEL(NAME, D, NQ, NS, CAUSAL, NSTAGE)                           \
+#define NC_FLASH_PIPE_KERNEL(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB)                      \
     extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) { \
-        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE>(a);                              \
+        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB>(a);                         \
     }
 
 // Pipelined variants: q = query waves (32 rows each), s = key-split waves, p = LDS ring depth.
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q8s1p3_full, 64, 8, 1, false, 3)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q8s1p3_causal, 64, 8, 1, true, 3)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_full, 64, 4, 1, false, 3)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_causal, 64, 4, 1, true, 3)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_full, 64, 2, 4, false, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_causal, 64, 2, 4, true, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_full, 64, 1, 8, false, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_causal, 64, 1, 8, true, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_full, 32, 4, 1, false, 3)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_causal, 32, 4, 1, true, 3)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_full, 32, 2, 4, false, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_causal, 32, 2, 4, true, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p2_full, 32, 1, 8, false, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p2_causal, 32, 1, 8, true, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_full, 16, 2, 4, false, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_causal, 16, 2, 4, true, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_full, 16, 1, 8, false, 2)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_causal, 16, 1, 8, true, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q8s1p3_full, 64, 8, 1, false, 3, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q8s1p3_causal, 64, 8, 1, true, 3, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_full, 64, 4, 1, false, 3, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_causal, 64, 4, 1, true, 3, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_full, 64, 2, 4, false, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_causal, 64, 2, 4, true, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_full, 64, 1, 8, false, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_causal, 64, 1, 8, true, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_full, 32, 4, 1, false, 3, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_causal, 32, 4, 1, true, 3, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_full, 32, 2, 4, false, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_causal, 32, 2, 4, true, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p2_full, 32, 1, 8, false, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p2_causal, 32, 1, 8, true, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_full, 16, 2, 4, false, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_causal, 16, 2, 4, true, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_full, 16, 1, 8, false, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_causal, 16, 1, 8, true, 2, 1)
+

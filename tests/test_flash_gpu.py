@@ -152,12 +152,15 @@ def test_each_kernel_variant_parity(gpu, name):
 
     d = int(re.search(r"_d(\d+)_", name).group(1))
     causal = "_causal" in name
-    m = re.search(r"_q(\d+)s(\d+)p\d+_", name)
+    m = re.search(r"_q(\d+)s(\d+)p\d+(?:x\d+)?_", name)
     bm, threads = (32 * int(m.group(1)), 64 * int(m.group(1)) * int(m.group(2))) if m else (64, 256)
-    wl = Workload(f"variant_{name}", 3, 333, d, causal, 1.0 / math.sqrt(d), (("normal", 0.0, 1.0),) * 3, seed=21)
+    # S = 1100: every wave of every variant (up to 512 keys per staged block) steps through
+    # several blocks, so ring reuse and refills are exercised; S is not a multiple of any tile.
+    s = 1100
+    wl = Workload(f"variant_{name}", 2, s, d, causal, 1.0 / math.sqrt(d), (("normal", 0.0, 1.0),) * 3, seed=21)
     if name.endswith("_unaligned"):
-        wl.q_stride = wl.k_stride = wl.v_stride = 333 * d + 3
-        wl.o_stride = 333 * d + 5
+        wl.q_stride = wl.k_stride = wl.v_stride = s * d + 3
+        wl.o_stride = s * d + 5
     say(f"[case] {name} bm={bm} threads={threads}")
     q, k, v = wl.make_inputs()
     o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
