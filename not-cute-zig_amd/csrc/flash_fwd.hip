@@ -43,7 +43,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (P <= 2^8)
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
@@ -400,6 +399,11 @@ struct Swz {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
+// The same descriptor as four words, for buffer instructions issued through asm.
+__device__ __forceinline__ u32x4 rsrc_words(const void *base, uint32_t bytes) {
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
+}
 
 // s_waitcnt vmcnt(n) with lgkmcnt(0), then a plain workgroup barrier (no memory fence, so loads of
 // later blocks stay in flight). The asm memory clobber keeps the compiler from moving LDS accesses
@@ -418,29 +422,6 @@ __device__ __forceinline__ void wait_vm_only() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xf) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
     asm volatile("" ::: "memory");
-}
-
-template <int LPW, int NSTAGE>
-__device__ __forceinline__ void wait_vm_own(int ahead) {
-    if constexpr (NSTAGE >= 4) {
-        if (ahead >= 2) { wait_vm_only<2 * LPW>(); return; }
-    }
-    if constexpr (NSTAGE >= 3) {
-        if (ahead >= 1) { wait_vm_only<LPW>(); return; }
-    }
-    wait_vm_only<0>();
-}
-
-template <int LPW, int NSTAGE>
-__device__ __forceinline__ void wait_block(int ahead) {
-    // ahead = blocks issued after the one about to be consumed (0 .. NSTAGE-2)
-    if constexpr (NSTAGE >= 4) {
-        if (ahead >= 2) { wait_vm_barrier<2 * LPW>(); return; }
-    }
-    if constexpr (NSTAGE >= 3) {
-        if (ahead >= 1) { wait_vm_barrier<LPW>(); return; }
-    }
-    wait_vm_barrier<0>();
 }
 
 // An empty asm statement that consumes the K fragments: every compiler-issued K read has then
@@ -480,6 +461,46 @@ __device__ __forceinline__ void static_for(F &&f) {
         f(IC<B>{});
         static_for<B + 1, E>(f);
     }
+}
+
+// Calls f(IC<A>{}) with A = clamp(x, LO, HI) for a uniform x (a chain of scalar branches).
+template <int LO, int HI, typename F>
+__device__ __forceinline__ void with_clamped(int x, F &&f) {
+    if constexpr (LO >= HI) {
+        f(IC<HI>{});
+    } else {
+        if (x <= LO) {
+            f(IC<LO>{});
+            return;
+        }
+        with_clamped<LO + 1, HI>(x, f);
+    }
+}
+
+// s_waitcnt vmcnt(ahead * LPW) [+ s_barrier] for a uniform ahead in [0, MAXA]: the wave's (or,
+// with the barrier, every wave's) loads of the block about to be consumed have landed while the
+// loads of the `ahead` blocks issued after it may still be in flight.
+template <int LPW, int MAXA>
+__device__ __forceinline__ void wait_vm_own(int ahead) {
+    with_clamped<0, MAXA>(ahead, [](auto ac) { wait_vm_only<decltype(ac)::value * LPW>(); });
+}
+template <int LPW, int MAXA>
+__device__ __forceinline__ void wait_block(int ahead) {
+    with_clamped<0, MAXA>(ahead, [](auto ac) { wait_vm_barrier<decltype(ac)::value * LPW>(); });
+}
+
+// 16-byte buffer load into registers through asm. The compiler does not track it, so it never
+// places a vmcnt wait of its own for the result; the caller waits with s_waitcnt and then ties
+// the registers to that wait (tie_regs). (A compiler-tracked load of loop-invariant registers
+// made the compiler wait, inside the loop, on every vm operation issued before the first use,
+// including the prefetch issued a few instructions earlier.)
+__device__ __forceinline__ void buffer_load_b128_asm(half8 &dst, u32x4 rsrc, uint32_t voff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(dst) : "v"(voff), "s"(rsrc));
+}
+template <int N>
+__device__ __forceinline__ void tie_regs(half8 (&r)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(r[i]));
 }
 
 // LDS reads at a lane address plus a compile-time byte offset (folded into the instruction's
@@ -522,7 +543,7 @@ template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB>
 __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &a) {
     using C = PipeCfg<D, NQ, NS, NSTAGE, SUB>;
     using SW = Swz<D>;
-    static_assert(NSTAGE >= 1 && NSTAGE <= 4, "ring depth");
+    static_assert(NSTAGE >= 1 && NSTAGE <= 8, "ring depth");
     __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
 
     if (a.head_dim != (uint64_t)D || a.seq_len == 0) return;
@@ -559,18 +580,16 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     const uint32_t qspan = (uint32_t)((S - 1) * (uint64_t)a.q_row_stride + D) * 2;
     const uint32_t kspan = (uint32_t)((S - 1) * (uint64_t)a.k_row_stride + D) * 2;
     const uint32_t vspan = (uint32_t)((S - 1) * (uint64_t)a.v_row_stride + D) * 2;
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + (size_t)head * a.q_stride, qspan);
+    const u32x4 qr = rsrc_words(a.q + (size_t)head * a.q_stride, qspan);
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.k + (size_t)head * a.k_stride, kspan);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v + (size_t)head * a.v_stride, vspan);
     float *obase = a.o + (size_t)head * a.o_stride;
     const size_t ors = a.o_row_stride;
 
-    // Q^T B-operand (rows past seq_len read as zero).
+    // Q^T B-operand (rows past seq_len read as zero), waited for after the prologue.
     half8 qf[D / 16];
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-        qf[kk] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
-                                               qr, (uint32_t)qrow * qrb + (16 * kk + 8 * hh) * 2, 0, 0));
+    for (int kk = 0; kk < D / 16; ++kk) buffer_load_b128_asm(qf[kk], qr, (uint32_t)qrow * qrb + (16 * kk + 8 * hh) * 2);
 
     // One query group per workgroup: every wave consumes only its own key slice of each block,
     // so each wave stages that slice itself and no barrier is needed until the epilogue; a wave
@@ -635,13 +654,11 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // a zero scale by a tiny positive one (every score then rounds to weight exp2(0) = 1, as with
     // a zero scale), so the softmax below can assume sc > 0.
     float sc = a.scale * kLog2e;
-    if (sc < 0.f) {
-        sc = -sc;
-#pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) qf[kk] = -qf[kk];
-    }
+    const bool neg_q = sc < 0.f;  // Q is negated once it has landed
+    if (neg_q) sc = -sc;
     if (!(sc > 0.f) && sc == 0.f) sc = 1e-30f;
-    float mrow = neg_inf();
+    float mrow = neg_inf();  // running max of sc * score (log2 domain); -inf: none yet
+    float neg_m = 0.f;       // -mrow, 0 while mrow is -inf
     float l = 0.f;
     floatx16 o[C::MT];
 #pragma unroll
@@ -657,7 +674,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             if (blk > 0) issue(blk, IC<0>{});
             wait_vm_only<0>();
         } else if constexpr (PRIV) {
-            wait_vm_own<C::LPW, NSTAGE>(min(NSTAGE - 2, nblk - 1 - blk));
+            wait_vm_own<C::LPW, NSTAGE - 2>(min(NSTAGE - 2, nblk - 1 - blk));
             if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
         } else if constexpr (NSTAGE == 1) {
             // Single stage: refill it once every wave is done with the previous block.
@@ -668,7 +685,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             }
             wait_vm_barrier<0>();
         } else {
-            wait_block<C::LPW, NSTAGE>(min(NSTAGE - 2, nblk - 1 - blk));
+            wait_block<C::LPW, NSTAGE - 2>(min(NSTAGE - 2, nblk - 1 - blk));
             if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
         }
 
@@ -708,10 +725,14 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             }
         });
 
-        // Online softmax on raw scores (sc > 0): the max is taken before scaling, which is exact
-        // because rounding is monotonic, and scale + subtract fuse into one FMA. The running max
-        // only moves (and O, l are rescaled) when some lane's max grows by more than 2^8, so P
-        // stays <= 256 (exact in f16 range) and the 32-multiply O rescale is rare.
+        // Online softmax (sc > 0). P = exp2(sc * s - m) is formed against the running max m as it
+        // stands and rounded to f16 for the PV product; the row sum adds the rounded weights
+        // (v_dot2c against 1.0 pairs), so numerator and denominator use the same P. f16 keeps
+        // its relative precision up to 65504, so m only has to move when some weight overflows
+        // f16, which makes that lane's tile sum infinite; then (and while a row has no max yet)
+        // the tile max is taken - before scaling, exact since rounding is monotonic - O and l
+        // are rescaled and the tile is redone. Once a row has a max its sum is >= 1, so small
+        // weights cannot underflow it.
         const bool need_mask = (kt0 + C::WK > S) || (CAUSAL && kt0 + C::WK - 1 > qw0);
         if (need_mask) {
             const int lim = CAUSAL ? min(qrow, S - 1) - kt0 : S - 1 - kt0;  // last visible key offset
@@ -721,46 +742,56 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 for (int r = 0; r < 16; ++r)
                     if (32 * j + 8 * (r >> 2) + 4 * hh + (r & 3) > lim) acc[j][r] = neg_inf();
         }
-        float mj[SUB];
+        half8 pf[SUB][2];
+        auto weights = [&]() {
+            const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+            float ls = 0.f;
 #pragma unroll
-        for (int j = 0; j < SUB; ++j) {
-            const floatx16 &x = acc[j];
-            const float m0 = fmaxf(fmaxf(x[0], x[1]), x[2]), m1 = fmaxf(fmaxf(x[3], x[4]), x[5]);
-            const float m2 = fmaxf(fmaxf(x[6], x[7]), x[8]), m3 = fmaxf(fmaxf(x[9], x[10]), x[11]);
-            const float m4 = fmaxf(fmaxf(x[12], x[13]), x[14]);
-            mj[j] = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), x[15]));
-        }
-        float tmax = mj[0];
+            for (int j = 0; j < SUB; ++j)
 #pragma unroll
-        for (int j = 1; j < SUB; ++j) tmax = fmaxf(tmax, mj[j]);
-        const float m_tile = pair_max(tmax) * sc;
-        if (__builtin_amdgcn_ballot_w64(m_tile > mrow + kRescaleLog2)) {
-            const float m_new = fmaxf(mrow, m_tile);
+                for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                    for (int r = 0; r < 8; ++r)
+                        pf[j][ks][r] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][8 * ks + r], sc, neg_m));
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const half2v h = {pf[j][ks][2 * t], pf[j][ks][2 * t + 1]};
+                        ls = __builtin_amdgcn_fdot2(h, ones, ls, false);
+                    }
+                }
+            return ls;
+        };
+        // Move the running max to the tile max (rows whose max does not grow keep it) and rescale.
+        auto to_tile_max = [&]() {
+            float tmax = neg_inf();
+#pragma unroll
+            for (int j = 0; j < SUB; ++j) {
+                const floatx16 &x = acc[j];
+                const float m0 = fmaxf(fmaxf(x[0], x[1]), x[2]), m1 = fmaxf(fmaxf(x[3], x[4]), x[5]);
+                const float m2 = fmaxf(fmaxf(x[6], x[7]), x[8]), m3 = fmaxf(fmaxf(x[9], x[10]), x[11]);
+                const float m4 = fmaxf(fmaxf(x[12], x[13]), x[14]);
+                tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), x[15])));
+            }
+            const float m_new = fmaxf(mrow, pair_max(tmax) * sc);
             const float alpha = __builtin_amdgcn_exp2f(mrow - (m_new == neg_inf() ? 0.f : m_new));
             l *= alpha;
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt) o[mt] *= alpha;
             mrow = m_new;
+            neg_m = (mrow == neg_inf()) ? 0.f : -mrow;
+        };
+        float ls;
+        if (__builtin_amdgcn_ballot_w64(mrow == neg_inf())) {
+            to_tile_max();  // some row has no max yet: take it first
+            ls = weights();
+        } else {
+            ls = weights();
+            if (__builtin_amdgcn_ballot_w64(!(ls < __builtin_inff()))) {
+                to_tile_max();  // a weight overflowed f16: redo the tile against the new max
+                ls = weights();
+            }
         }
-        const float neg_m = (mrow == neg_inf()) ? 0.f : -mrow;
-        half8 pf[SUB][2];
-#pragma unroll
-        for (int j = 0; j < SUB; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                pf[j][r >> 3][r & 7] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][r], sc, neg_m));
-        // Row sum of the weights as rounded for the PV product (v_dot2c against 1.0 pairs); the
-        // numerator and the denominator then use the same P.
-        const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-        for (int j = 0; j < SUB; ++j)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const half2v h = {pf[j][ks][2 * t], pf[j][ks][2 * t + 1]};
-                    l = __builtin_amdgcn_fdot2(h, ones, l, false);
-                }
+        l += ls;
 
         wait_lds_tied(vt);
 #pragma unroll
@@ -775,19 +806,24 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 }
     };
 
-    if (nblk > 0) issue(0, IC<0>{});
-    if constexpr (NSTAGE > 2)
-        if (1 < nblk) issue(1, IC<1>{});
-    if constexpr (NSTAGE > 3)
-        if (2 < nblk) issue(2, IC<2>{});
+    // Prologue: blocks 0 .. NSTAGE-2 in flight; then Q (issued before them) has landed once at most
+    // their loads are outstanding.
+    static_for<0, (NSTAGE > 1 ? NSTAGE - 1 : 1)>([&](auto ic) {
+        constexpr int I = decltype(ic)::value;
+        if (I < nblk) issue(I, IC<I>{});
+    });
+    with_clamped<0, (NSTAGE > 1 ? NSTAGE - 1 : 1)>(nblk, [&](auto ac) { wait_vm_only<decltype(ac)::value * C::LPW>(); });
+    tie_regs(qf);
+    if (neg_q) {
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) qf[kk] = -qf[kk];
+    }
     for (int blk0 = 0; blk0 < nblk; blk0 += NSTAGE) {
         step(blk0, IC<0>{});
-        if constexpr (NSTAGE > 1)
-            if (blk0 + 1 < nblk) step(blk0 + 1, IC<1>{});
-        if constexpr (NSTAGE > 2)
-            if (blk0 + 2 < nblk) step(blk0 + 2, IC<2>{});
-        if constexpr (NSTAGE > 3)
-            if (blk0 + 3 < nblk) step(blk0 + 3, IC<3>{});
+        static_for<1, NSTAGE>([&](auto ic) {
+            constexpr int I = decltype(ic)::value;
+            if (blk0 + I < nblk) step(blk0 + I, IC<I>{});
+        });
     }
 
     // Epilogue. (1) Each wave publishes its per-query (m, l) in a dedicated LDS area (no wave
@@ -879,10 +915,17 @@ extern "C" __global__ __launch_bounds__(256) void nc_util_copy_b128(const u32x4 
     extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) { \
         flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB>(a);                         \
     }
+// With a register budget held to WPE waves per SIMD (512 / WPE VGPRs per wave): two 8-wave
+// workgroups of the 70 KB-LDS variants share a CU only if each wave fits in 128 VGPRs.
+#define NC_FLASH_PIPE_KERNEL_WPE(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB, WPE)                         \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) __attribute__((amdgpu_waves_per_eu(WPE))) \
+    void NAME(nc_flash_kernel_args a) {                                                             \
+        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB>(a);                                     \
+    }
 
 // Pipelined variants: q = query waves (32 rows each), s = key-split waves, p = LDS ring depth.
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q8s1p3_full, 64, 8, 1, false, 3, 1)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q8s1p3_causal, 64, 8, 1, true, 3, 1)
+NC_FLASH_PIPE_KERNEL_WPE(nc_flash_fwd_d64_q8s1p3_full, 64, 8, 1, false, 3, 1, 4)
+NC_FLASH_PIPE_KERNEL_WPE(nc_flash_fwd_d64_q8s1p3_causal, 64, 8, 1, true, 3, 1, 4)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_full, 64, 4, 1, false, 3, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_causal, 64, 4, 1, true, 3, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_full, 64, 2, 4, false, 2, 1)

@@ -141,7 +141,7 @@ def _variant_names():
     import re
     import os
     src = open(os.path.join(os.path.dirname(__file__), "..", "not-cute-zig_amd", "csrc", "flash_fwd.hip")).read()
-    return sorted(set(re.findall(r"NC_FLASH_(?:PIPE_)?KERNEL\((nc_flash_fwd_\w+),", src)))
+    return sorted(set(re.findall(r"NC_FLASH_(?:PIPE_)?KERNEL(?:_WPE)?\((nc_flash_fwd_\w+),", src)))
 
 
 @pytest.mark.parametrize("name", _variant_names())
