@@ -120,6 +120,26 @@ typedef struct nc_function_attributes {
 } nc_function_attributes;
 int nc_function_get_attributes(nc_function fn, nc_function_attributes *out);
 
+/* cuda.OccupancyCalculator.init (src/cuda.zig:228-245) over cuda.getDevice: the device limits the
+ * reference's profile-flash occupancy arithmetic uses (src/main.zig:96-104), for device 0, plus the
+ * gfx950 facts that arithmetic needs here (LDS per CU, SIMDs per CU, name). "SM" is a CU. */
+typedef struct nc_device_attributes {
+    int32_t max_threads_per_block;
+    int32_t max_shared_memory_per_block; /* bytes of LDS one workgroup may use */
+    int32_t max_registers_per_sm;        /* 32-bit VGPR lanes per CU (hipDeviceProp regsPerMultiprocessor) */
+    int32_t max_threads_per_sm;
+    int32_t sm_count;                    /* CUs */
+    int32_t warp_size;                   /* 64 */
+    int32_t max_shared_memory_per_sm;    /* LDS per CU, bytes */
+    int32_t clock_khz;                   /* peak shader clock */
+    char name[64];                       /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+} nc_device_attributes;
+int nc_device_get_attributes(nc_device_attributes *out);
+/* Workgroups of `block_threads` threads that fit on one CU at once
+ * (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor). An extension: the reference derives this by
+ * hand from the function attributes and the device limits (src/main.zig:96-104). */
+int nc_function_max_active_blocks(nc_function fn, int block_threads, size_t dynamic_shared_bytes, int *blocks);
+
 /* Stream (src/cuda.zig:319-341). Created non-blocking at the default priority. */
 int nc_stream_create(nc_stream *out);
 int nc_stream_destroy(nc_stream stream);

@@ -243,6 +243,38 @@ int nc_function_get_attributes(nc_function fn, nc_function_attributes *out) {
     return NC_SUCCESS;
 }
 
+int nc_device_get_attributes(nc_device_attributes *out) {
+    if (!out) return fail(NC_ERROR_INVALID_VALUE, "nc_device_get_attributes: null output");
+    std::memset(out, 0, sizeof *out);
+    int st = nc_init();
+    if (st) return st;
+    hipDeviceProp_t p;
+    st = check(hipGetDeviceProperties(&p, 0), "hipGetDeviceProperties");
+    if (st) return st;
+    out->max_threads_per_block = p.maxThreadsPerBlock;
+    out->max_shared_memory_per_block = (int32_t)p.sharedMemPerBlock;
+    out->max_registers_per_sm = p.regsPerMultiprocessor;
+    out->max_threads_per_sm = p.maxThreadsPerMultiProcessor;
+    out->sm_count = p.multiProcessorCount;
+    out->warp_size = p.warpSize;
+    out->max_shared_memory_per_sm = (int32_t)p.maxSharedMemoryPerMultiProcessor;
+    out->clock_khz = p.clockRate;
+    std::snprintf(out->name, sizeof out->name, "%.63s", p.gcnArchName);
+    return NC_SUCCESS;
+}
+
+int nc_function_max_active_blocks(nc_function fn, int block_threads, size_t dynamic_shared_bytes, int *blocks) {
+    if (!fn || !blocks || block_threads <= 0)
+        return fail(NC_ERROR_INVALID_VALUE, "nc_function_max_active_blocks: invalid argument");
+    *blocks = 0;
+    int n = 0;
+    int st = check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn->fn, block_threads, dynamic_shared_bytes),
+                   "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (st) return st;
+    *blocks = n;
+    return NC_SUCCESS;
+}
+
 int nc_stream_create(nc_stream *out) {
     if (!out) return fail(NC_ERROR_INVALID_VALUE, "nc_stream_create: null output");
     hipStream_t s = nullptr;

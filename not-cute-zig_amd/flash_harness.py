@@ -1,0 +1,463 @@
+#!/usr/bin/env python3
+"""Command-line harness for the flash path, mirroring the reference's `flash`, `compare`,
+`profile-flash` and flash-benchmark commands (src/main.zig:53-62) and the compare table of its
+runner (modal_run.py:34-69), on one MI355X through the C ABI.
+
+    python flash_harness.py flash                 # runFlashAttention's four cases (src/main.zig:189-194)
+    python flash_harness.py compare               # runCompareDemo's flash shapes as JSONL (src/main.zig:141-170)
+    python flash_harness.py baselines             # PyTorch SDPA on the same shapes (tools/pytorch_baselines.py)
+    python flash_harness.py profile-flash         # runProfileFlash (src/main.zig:81-130)
+    python flash_harness.py benchmark-flash       # runFlashBenchmark (src/main.zig:760-766)
+    python flash_harness.py compare-table FILE... # the baseline-vs-not-cute table (modal_run.py:34-69)
+
+Correctness here is checked against a float64 softmax(scale * Q K^T) V written in this file (the
+reference checks against its f32 CPU loop; both are far inside the 0.008 / 0.02 tolerances it
+applies). `baselines` times PyTorch's scaled_dot_product_attention backends on the same device,
+shapes and inputs, in its own process: PyTorch brings its own HIP runtime, and this library is then
+used only for its host-side input fills.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+from typing import Dict, Iterable, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+import notcute_flash as nc  # noqa: E402
+from flash_workloads import REFERENCE_COMPARE_SHAPES, REFERENCE_FILLS, Workload, reference_smoke_cases  # noqa: E402
+
+# runFlashBenchmark's cases (src/main.zig:760-766) and their fills (src/main.zig:787-795):
+# Q = ((3i+1) % 11) / 8, K = ((5i+2) % 13) / 16, V = ((7i+3) % 17) / 32.
+BENCHMARK_SHAPES = [(2, 32, 16, False), (2, 32, 32, True), (2, 64, 16, False), (2, 64, 32, True), (2, 128, 32, True)]
+BENCHMARK_FILLS = ((3, 1, 11, 0.125), (5, 2, 13, 0.0625), (7, 3, 17, 0.03125))
+
+SMOKE_TOL = 0.008    # src/main.zig:279
+COMPARE_TOL = 0.02   # src/main.zig:1042
+BASELINE_TOL = 0.08  # tools/pytorch_baselines.py:205
+
+# Keys of a compare record, in the reference's order (src/main.zig:873-880).
+RECORD_KEYS = ("kernel", "implementation", "shape", "correct", "mean_ms", "min_ms", "max_ms", "gbps", "tflops",
+               "bytes", "flops", "max_abs_error")
+
+
+def shape_name(batch_heads: int, seq_len: int, head_dim: int, causal: bool) -> str:
+    """src/main.zig:1044 / tools/pytorch_baselines.py:50."""
+    return f"batch_heads={batch_heads},seq={seq_len},head={head_dim},causal={str(causal).lower()}"
+
+
+def reference_work(batch_heads: int, seq_len: int, head_dim: int, causal: bool) -> Tuple[int, int]:
+    """(flops, bytes) as src/main.zig:1032-1034: S(S+1)/2 score pairs when causal."""
+    eff = seq_len * (seq_len + 1) // 2 if causal else seq_len * seq_len
+    return batch_heads * 4 * eff * head_dim, batch_heads * seq_len * head_dim * (2 * 3 + 4)
+
+
+def modular_fill(n: int, mul: int, add: int, mod: int, scale: float) -> np.ndarray:
+    """f16 bit patterns of ((i*mul + add) % mod) * scale, i = 0..n-1."""
+    i = np.arange(n, dtype=np.int64)
+    return ((((i * mul + add) % mod).astype(np.float32)) * np.float32(scale)).astype(np.float16).view(np.uint16)
+
+
+def attention_f64(wl: Workload, q: np.ndarray, k: np.ndarray, v: np.ndarray,
+                  rows: Optional[np.ndarray] = None) -> np.ndarray:
+    """softmax(scale * Q K^T, causal mask) V in float64 for every slice; returns O in the workload's
+    f32 layout with unwritten (pad) positions left 0. `rows` restricts the query rows computed."""
+    S, D = wl.seq_len, wl.head_dim
+    out = np.zeros(wl.length("o"), dtype=np.float64)
+    qf, kf, vf = (x.view(np.float16).astype(np.float64) for x in (q, k, v))
+    r_all = np.arange(S) if rows is None else np.asarray(rows)
+    for b in range(wl.batch_heads):
+        def mat(buf, which):
+            base, rs = b * wl.stride(which), wl.row(which)
+            idx = base + np.arange(S)[:, None] * rs + np.arange(D)[None, :]
+            return buf[idx]
+        Q, K, V = mat(qf, "q")[r_all], mat(kf, "k"), mat(vf, "v")
+        s = (Q @ K.T) * float(np.float32(wl.scale))
+        if wl.causal:
+            s = np.where(np.arange(S)[None, :] > r_all[:, None], -np.inf, s)
+        s = s - s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        o = (p / p.sum(axis=1, keepdims=True)) @ V
+        obase, ors = b * wl.stride("o"), wl.row("o")
+        out[obase + r_all[:, None] * ors + np.arange(D)[None, :]] = o
+    return out
+
+
+def active_index(wl: Workload, rows: Optional[np.ndarray] = None) -> np.ndarray:
+    S, D = wl.seq_len, wl.head_dim
+    r = np.arange(S) if rows is None else np.asarray(rows)
+    idx = [b * wl.stride("o") + r[:, None] * wl.row("o") + np.arange(D)[None, :] for b in range(wl.batch_heads)]
+    return np.concatenate([x.ravel() for x in idx])
+
+
+def make_record(implementation: str, shape: str, correct: bool, mean_ms: float, min_ms: float, max_ms: float,
+                bytes_: int, flops: int, max_abs_error: float) -> Dict:
+    """One compare record with the reference's fields and formulas (src/benchmark.zig:83-89)."""
+    gbps = bytes_ / (mean_ms * 1.0e6) if mean_ms > 0 else 0.0
+    tflops = flops / (mean_ms * 1.0e9) if mean_ms > 0 else 0.0
+    vals = ("flash_attention", implementation, shape, bool(correct), float(mean_ms), float(min_ms), float(max_ms),
+            gbps, tflops, int(bytes_), int(flops), float(max_abs_error))
+    return dict(zip(RECORD_KEYS, vals))
+
+
+def emit(rec: Dict, out=None) -> None:
+    out = sys.stdout if out is None else out
+    out.write(json.dumps(rec, separators=(",", ":")) + "\n")
+    out.flush()
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Device:
+    """Device buffers of one workload's inputs and output, uploaded once."""
+
+    def __init__(self, wl: Workload, q, k, v, o_init=None):
+        self.wl = wl
+        self.bufs = [nc.DeviceBuffer.from_array(x) for x in (q, k, v)]
+        o = np.zeros(wl.length("o"), np.float32) if o_init is None else o_init
+        self.bufs.append(nc.DeviceBuffer.from_array(o))
+
+    def launch(self, module: nc.Module) -> None:
+        q, k, v, o = self.bufs
+        nc.flash_launch(module, q, k, v, o, self.wl.options())
+
+    def output(self) -> np.ndarray:
+        nc.synchronize()
+        return self.bufs[3].download(np.float32, self.wl.length("o"))
+
+    def time_selected(self, module: nc.Module, flops: int, bytes_: int, warmup: int = 5, iters: int = 20):
+        """benchmark.runKernel over the selected kernel (src/main.zig:1033-1035)."""
+        opts = self.wl.options()
+        sel = nc.select_kernel(opts)
+        fn = module.get_function(sel.name.decode())
+        args = nc.pack_args(opts, sel, *[b.ptr for b in self.bufs])
+        return sel, nc.run_kernel(fn, tuple(sel.grid), (sel.threads,), [args], warmup=warmup, iters=iters,
+                                  bytes_=bytes_, flops=flops)
+
+    def free(self) -> None:
+        for b in self.bufs:
+            b.free()
+
+
+# ---------------------------------------------------------------------------------------------
+# flash: runFlashAttention (src/main.zig:189-287)
+# ---------------------------------------------------------------------------------------------
+
+def cmd_flash(module: nc.Module, _args) -> int:
+    status = 0
+    for wl in reference_smoke_cases():
+        q, k, v = wl.make_inputs()
+        dev = Device(wl, q, k, v)
+        try:
+            dev.launch(module)
+            out = dev.output()
+        finally:
+            dev.free()
+        ref = attention_f64(wl, q, k, v)
+        idx = active_index(wl)
+        diff = np.abs(out[idx] - ref[idx])
+        bad = np.nonzero(diff > SMOKE_TOL)[0]
+        pad = np.setdiff1d(np.arange(wl.length("o")), idx)
+        if bad.size:
+            i = int(idx[bad[0]])
+            b = i // wl.stride("o")
+            log(f"flash mismatch at batch {b} idx {i - b * wl.stride('o')}: expected {ref[i]}, got {out[i]}, "
+                f"diff {abs(out[i] - ref[i])}")
+            status = 1
+        elif pad.size and np.any(out[pad] != 0):
+            log(f"flash wrote outside the active region: batch_heads={wl.batch_heads}, seq={wl.seq_len}")
+            status = 1
+        else:
+            log(f"flash attention OK: batch_heads={wl.batch_heads}, causal={str(wl.causal).lower()}, "
+                f"Q/K/V/O={wl.seq_len}x{wl.head_dim} (max-abs {float(diff.max()):.2e})")
+    return status
+
+
+# ---------------------------------------------------------------------------------------------
+# compare: compareFlash (src/main.zig:976-1047) + tools/pytorch_baselines.py
+# ---------------------------------------------------------------------------------------------
+
+def compare_workloads(which: str) -> List[Tuple[Workload, Optional[np.ndarray]]]:
+    """(workload, checked rows or None for all)."""
+    if which == "reference":
+        return [(Workload(f"compare_bh{bh}_s{s}_d{d}", bh, s, d, c, 1.0 / math.sqrt(d), REFERENCE_FILLS), None)
+                for (bh, s, d, c) in REFERENCE_COMPARE_SHAPES]
+    from flash_workloads import CONFIGS, sample_rows
+    out = []
+    for name in ("c1", "c3", "c4", "c5"):
+        wl = CONFIGS[name]
+        out.append((wl, None if wl.seq_len <= 1024 else sample_rows(wl.seq_len, extra=16, seed=wl.seed)))
+    return out
+
+
+def torch_baselines(wl: Workload, q, k, v, ref: np.ndarray, idx: np.ndarray, shape: str, flops: int, bytes_: int,
+                    warmup: int, iters: int) -> List[Dict]:
+    """scaled_dot_product_attention backends on the same device and inputs (contiguous slices
+    only). The math backend runs on float32 copies: its batched products in reduced precision take
+    transposed views, which this pool's GPUs do not run reliably."""
+    try:
+        import torch
+        import torch.nn.functional as F
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+    except Exception as exc:  # torch absent or too old
+        log(f"baselines skipped: {exc}")
+        return []
+    if not torch.cuda.is_available():
+        log("baselines skipped: torch sees no GPU")
+        return []
+    if any(wl.stride(x) != wl.seq_len * wl.head_dim for x in "qkvo"):
+        log(f"baselines skipped for {shape}: padded slices")
+        return []
+    B, S, D = wl.batch_heads, wl.seq_len, wl.head_dim
+
+    def t(x):
+        return torch.from_numpy(x.view(np.float16).reshape(B, 1, S, D).copy()).to("cuda")
+
+    tq, tk, tv = t(q), t(k), t(v)
+    scale = float(np.float32(wl.scale))
+    recs = []
+    for impl, backend, dtype in (("torch_sdpa_flash", SDPBackend.FLASH_ATTENTION, torch.float16),
+                                 ("torch_sdpa_mem_efficient", SDPBackend.EFFICIENT_ATTENTION, torch.float16),
+                                 ("torch_sdpa_math_f32", SDPBackend.MATH, torch.float32)):
+        a, b_, c_ = (x.to(dtype) for x in (tq, tk, tv))
+        try:
+            with sdpa_kernel(backend):
+                for _ in range(warmup):
+                    o = F.scaled_dot_product_attention(a, b_, c_, is_causal=wl.causal, scale=scale)
+                torch.cuda.synchronize()
+                samples = []
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                for _ in range(iters):
+                    e0.record()
+                    o = F.scaled_dot_product_attention(a, b_, c_, is_causal=wl.causal, scale=scale)
+                    e1.record()
+                    e1.synchronize()
+                    samples.append(float(e0.elapsed_time(e1)))
+        except Exception as exc:
+            log(f"{impl} unavailable for {shape}: {str(exc).splitlines()[0][:160]}")
+            continue
+        got = o.to(torch.float32).reshape(-1).cpu().numpy().astype(np.float64)
+        err = float(np.max(np.abs(got[idx] - ref[idx])))
+        recs.append(make_record(impl, shape, err <= BASELINE_TOL, sum(samples) / len(samples), min(samples),
+                                max(samples), bytes_, flops, err))
+    return recs
+
+
+def cmd_compare(module: nc.Module, args) -> int:
+    status = 0
+    for wl, rows in compare_workloads(args.shapes):
+        shape = shape_name(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
+        flops, bytes_ = reference_work(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
+        q, k, v = wl.make_inputs()
+        dev = Device(wl, q, k, v)
+        try:
+            dev.launch(module)
+            out = dev.output()
+            sel, res = dev.time_selected(module, flops, bytes_, args.warmup, args.iters)
+        finally:
+            dev.free()
+        ref = attention_f64(wl, q, k, v, rows)
+        idx = np.arange(wl.length("o")) if rows is None else active_index(wl, rows)
+        err = float(np.max(np.abs(out[idx] - ref[idx])))
+        ok = err <= COMPARE_TOL
+        status |= 0 if ok else 1
+        log(f"compare: not-cute flash {shape} -> {sel.name.decode()}")
+        emit(make_record("not_cute", shape, ok, res.mean_ms, res.min_ms, res.max_ms, bytes_, flops, err))
+    return status
+
+
+def cmd_baselines(args) -> int:
+    """tools/pytorch_baselines.py over the same shapes and inputs as `compare`."""
+    import torch  # noqa: F401  (before any HIP use in this process)
+
+    cases = compare_workloads(args.shapes)
+    if args.limit:
+        cases = cases[:args.limit]
+    n = 0
+    for wl, rows in cases:
+        shape = shape_name(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
+        flops, bytes_ = reference_work(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
+        q, k, v = wl.make_inputs()
+        ref = attention_f64(wl, q, k, v, rows)
+        idx = np.arange(wl.length("o")) if rows is None else active_index(wl, rows)
+        for rec in torch_baselines(wl, q, k, v, ref, idx, shape, flops, bytes_, args.warmup, args.iters):
+            emit(rec)
+            n += 1
+    return 0 if n else 1
+
+
+# ---------------------------------------------------------------------------------------------
+# profile-flash: runProfileFlash (src/main.zig:81-130)
+# ---------------------------------------------------------------------------------------------
+
+def occupancy_report(module: nc.Module, opts) -> Dict:
+    sel = nc.select_kernel(opts)
+    fn = module.get_function(sel.name.decode())
+    attrs = fn.attributes()
+    dev = nc.device_attributes()
+    threads = int(sel.threads)
+    waves_per_block = threads // dev.warp_size
+    by_threads = dev.max_threads_per_sm // threads
+    regs_per_block = attrs.num_regs * threads
+    by_regs = dev.max_registers_per_sm // regs_per_block if regs_per_block > 0 else by_threads
+    by_lds = dev.max_shared_memory_per_sm // attrs.shared_size_bytes if attrs.shared_size_bytes > 0 else by_threads
+    selected = fn.max_active_blocks(threads)
+    return {
+        "kernel": sel.name.decode(), "label": sel.label.decode(), "threads": threads,
+        "grid": [int(x) for x in sel.grid], "regs_per_thread": attrs.num_regs,
+        "static_lds": attrs.shared_size_bytes, "local": attrs.local_size_bytes, "const": attrs.const_size_bytes,
+        "max_threads_per_block": attrs.max_threads_per_block, "binary_version": attrs.binary_version,
+        "limit_by_threads": by_threads, "limit_by_regs": by_regs, "limit_by_lds": by_lds,
+        "blocks_per_cu": selected, "waves_per_cu": selected * waves_per_block,
+        "max_waves_per_cu": dev.max_threads_per_sm // dev.warp_size, "cu_count": dev.sm_count,
+        "device": dev.name.decode(),
+    }
+
+
+def cmd_profile(module: nc.Module, args) -> int:
+    bh, s, d, causal = 8, 1024, 64, True
+    opts = nc.options(batch_heads=bh, seq_len=s, head_dim=d, scale=1.0 / math.sqrt(d), causal=causal)
+    r = occupancy_report(module, opts)
+    log(f"profile: not-cute flash batch_heads={bh} seq={s} head={d} causal=true")
+    log(f"profile: selected kernel {r['kernel']} ({r['label']}), threads/block={r['threads']}, grid={r['grid'][0]}")
+    log(f"profile: function attrs regs/thread={r['regs_per_thread']}, static_lds={r['static_lds']} B, "
+        f"local={r['local']} B, const={r['const']} B, max_threads/block={r['max_threads_per_block']}, "
+        f"binary={r['binary_version']}")
+    log(f"profile: occupancy limits blocks/CU threads={r['limit_by_threads']}, regs={r['limit_by_regs']}, "
+        f"lds={r['limit_by_lds']}, selected={r['blocks_per_cu']} (HIP occupancy API)")
+    log(f"profile: selected occupancy waves/CU={r['waves_per_cu']} of max {r['max_waves_per_cu']} "
+        f"on {r['cu_count']} CUs ({r['device']})")
+    print(json.dumps({"profile": r}, separators=(",", ":")), flush=True)
+    args.shapes = "single"
+    wl = Workload("profile", bh, s, d, causal, 1.0 / math.sqrt(d), REFERENCE_FILLS)
+    return _compare_one(module, wl, args)
+
+
+def _compare_one(module: nc.Module, wl: Workload, args) -> int:
+    shape = shape_name(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
+    flops, bytes_ = reference_work(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
+    q, k, v = wl.make_inputs()
+    dev = Device(wl, q, k, v)
+    try:
+        dev.launch(module)
+        out = dev.output()
+        _, res = dev.time_selected(module, flops, bytes_, args.warmup, args.iters)
+    finally:
+        dev.free()
+    err = float(np.max(np.abs(out - attention_f64(wl, q, k, v))))
+    emit(make_record("not_cute", shape, err <= COMPARE_TOL, res.mean_ms, res.min_ms, res.max_ms, bytes_, flops, err))
+    return 0 if err <= COMPARE_TOL else 1
+
+
+# ---------------------------------------------------------------------------------------------
+# benchmark-flash: runFlashBenchmark (src/main.zig:760-857) with BenchmarkResult.print
+# ---------------------------------------------------------------------------------------------
+
+def cmd_benchmark(module: nc.Module, args) -> int:
+    for (bh, s, d, causal) in BENCHMARK_SHAPES:
+        n = bh * s * d
+        q, k, v = (modular_fill(n, *f) for f in BENCHMARK_FILLS)
+        wl = Workload("bench", bh, s, d, causal, 1.0 / math.sqrt(d), REFERENCE_FILLS)
+        flops, bytes_ = reference_work(bh, s, d, causal)
+        dev = Device(wl, q, k, v)
+        try:
+            sel, res = dev.time_selected(module, flops, bytes_, args.warmup, args.iters)
+        finally:
+            dev.free()
+        print(f"--- Benchmark: {sel.label.decode()} seq={s} head={d} causal={str(causal).lower()} ---")
+        print(f"  Time: mean={res.mean_ms:.3f}ms, min={res.min_ms:.3f}ms, max={res.max_ms:.3f}ms")
+        print(f"  Bandwidth: {res.throughput_gbps:.2f} GB/s")
+        print(f"  Compute:   {res.tflops:.2f} TFLOPs", flush=True)
+    return 0
+
+
+# ---------------------------------------------------------------------------------------------
+# compare-table (modal_run.py:34-69)
+# ---------------------------------------------------------------------------------------------
+
+BASELINE_IMPLS = ("torch_sdpa_flash", "torch_sdpa_mem_efficient", "torch_sdpa_math", "torch_sdpa_math_f32",
+                  "cublas_materialized", "cuda_wmma", "cuda_tiled")
+
+
+def read_records(lines: Iterable[str]) -> List[Dict]:
+    recs = []
+    for line in lines:
+        line = line.strip()
+        if not line.startswith("{"):
+            continue
+        try:
+            r = json.loads(line)
+        except json.JSONDecodeError as exc:
+            log(f"skipping malformed JSONL record: {exc}: {line}")
+            continue
+        if "implementation" in r and "shape" in r:
+            recs.append(r)
+    return recs
+
+
+def compare_table(records: Sequence[Dict]) -> str:
+    by_case: Dict[Tuple[str, str], Dict[str, Dict]] = {}
+    for r in records:
+        by_case.setdefault((r["kernel"], r["shape"]), {})[r["implementation"]] = r
+    lines = ["=== baselines vs not-cute ===",
+             f"{'kernel':<18} {'shape':<40} {'baseline':<26} {'not-cute ms':>12} {'base ms':>12} {'speedup':>9} {'ok':>5}"]
+    for (kernel, shape), impls in sorted(by_case.items()):
+        mine = impls.get("not_cute")
+        if not mine:
+            continue
+        for impl in BASELINE_IMPLS:
+            base = impls.get(impl)
+            if not base:
+                continue
+            speedup = base["mean_ms"] / mine["mean_ms"] if mine["mean_ms"] else 0.0
+            ok = "yes" if mine["correct"] and base["correct"] else "no"
+            lines.append(f"{kernel:<18} {shape:<40} {impl:<26} {mine['mean_ms']:>12.6f} {base['mean_ms']:>12.6f} "
+                         f"{speedup:>8.2f}x {ok:>5}")
+    return "\n".join(lines)
+
+
+def cmd_table(args) -> int:
+    recs = []
+    for path in args.files:
+        with (sys.stdin if path == "-" else open(path)) as f:
+            recs.extend(read_records(f))
+    print(compare_table(recs))
+    return 0
+
+
+def main(argv: Optional[Sequence[str]] = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    sub.add_parser("flash", help="the reference's four flash smoke cases")
+    p = sub.add_parser("compare", help="compare records (JSONL on stdout)")
+    p.add_argument("--shapes", choices=("reference", "configs"), default="reference")
+    b = sub.add_parser("baselines", help="torch SDPA records for the compare shapes (JSONL on stdout)")
+    b.add_argument("--shapes", choices=("reference", "configs"), default="reference")
+    b.add_argument("--limit", type=int, default=0, help="only the first N shapes")
+    for q in (p, b, sub.add_parser("profile-flash", help="attributes and occupancy of the c3 kernel"),
+              sub.add_parser("benchmark-flash", help="runFlashBenchmark's five cases")):
+        q.add_argument("--warmup", type=int, default=5)
+        q.add_argument("--iters", type=int, default=20)
+    t = sub.add_parser("compare-table", help="print the baseline table from JSONL files ('-' = stdin)")
+    t.add_argument("files", nargs="+")
+    args = ap.parse_args(argv)
+    if args.cmd == "compare-table":
+        return cmd_table(args)
+    if args.cmd == "baselines":
+        return cmd_baselines(args)
+    nc.init()
+    module = nc.Module.load_embedded()
+    return {"flash": cmd_flash, "compare": cmd_compare, "profile-flash": cmd_profile,
+            "benchmark-flash": cmd_benchmark}[args.cmd](module, args)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

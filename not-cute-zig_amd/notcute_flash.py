@@ -127,6 +127,22 @@ class FunctionAttributes(ctypes.Structure):
     ]
 
 
+class DeviceAttributes(ctypes.Structure):
+    """cuda.OccupancyCalculator fields (src/cuda.zig:228-245) plus the gfx950 LDS/clock/name."""
+
+    _fields_ = [
+        ("max_threads_per_block", ctypes.c_int32),
+        ("max_shared_memory_per_block", ctypes.c_int32),
+        ("max_registers_per_sm", ctypes.c_int32),
+        ("max_threads_per_sm", ctypes.c_int32),
+        ("sm_count", ctypes.c_int32),
+        ("warp_size", ctypes.c_int32),
+        ("max_shared_memory_per_sm", ctypes.c_int32),
+        ("clock_khz", ctypes.c_int32),
+        ("name", ctypes.c_char * 64),
+    ]
+
+
 class FlashWork(ctypes.Structure):
     _fields_ = [
         ("flops_reference", ctypes.c_uint64),
@@ -184,6 +200,8 @@ _SIGS = {
     "nc_module_get_function": (ctypes.c_int, [ctypes.POINTER(_P), _P, ctypes.c_char_p]),
     "nc_function_launch": (ctypes.c_int, [_P, ctypes.POINTER(LaunchConfig), ctypes.POINTER(_P)]),
     "nc_function_get_attributes": (ctypes.c_int, [_P, ctypes.POINTER(FunctionAttributes)]),
+    "nc_device_get_attributes": (ctypes.c_int, [ctypes.POINTER(DeviceAttributes)]),
+    "nc_function_max_active_blocks": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]),
     "nc_stream_create": (ctypes.c_int, [ctypes.POINTER(_P)]),
     "nc_stream_destroy": (ctypes.c_int, [_P]),
     "nc_stream_synchronize": (ctypes.c_int, [_P]),
@@ -388,11 +406,25 @@ class Function:
         check(lib().nc_function_get_attributes(self.handle, ctypes.byref(a)), "Function.getAttributes")
         return a
 
+    def max_active_blocks(self, block_threads: int, dynamic_shared_bytes: int = 0) -> int:
+        """Workgroups of `block_threads` threads resident on one CU at once."""
+        n = ctypes.c_int(0)
+        check(lib().nc_function_max_active_blocks(self.handle, block_threads, dynamic_shared_bytes, ctypes.byref(n)),
+              f"occupancy({self.name})")
+        return n.value
+
     def launch(self, grid: Sequence[int], block: Sequence[int], params: Sequence[ctypes._SimpleCData],
                stream: Optional[int] = None, shared_mem_bytes: int = 0) -> None:
         cfg = make_config(grid, block, stream, shared_mem_bytes)
         arr = (ctypes.c_void_p * len(params))(*[ctypes.cast(ctypes.pointer(p), ctypes.c_void_p) for p in params])
         check(lib().nc_function_launch(self.handle, ctypes.byref(cfg), arr), f"Function.launch({self.name})")
+
+
+def device_attributes() -> DeviceAttributes:
+    """cuda.getDevice + OccupancyCalculator.init (src/cuda.zig:228-245) for device 0."""
+    a = DeviceAttributes()
+    check(lib().nc_device_get_attributes(ctypes.byref(a)), "device attributes")
+    return a
 
 
 def make_config(grid: Sequence[int], block: Sequence[int], stream: Optional[int] = None,

@@ -1,0 +1,89 @@
+"""Host-side tests of the flash harness CLI (not-cute-zig_amd/flash_harness.py): its float64
+reference against the CPU oracle, the compare-record format of src/main.zig:859-881, the compare
+table of modal_run.py:34-69, and runFlashBenchmark's fills (src/main.zig:787-795)."""
+
+import io
+import json
+import math
+
+import numpy as np
+import pytest
+
+import flash_harness as fh
+import flashcheck as fc
+from flash_workloads import REFERENCE_FILLS, Workload, reference_smoke_cases
+
+
+@pytest.mark.parametrize("wl", [
+    Workload("h_nc", 2, 37, 16, False, 0.25, (("normal", 0.0, 1.0),) * 3, seed=5),
+    Workload("h_c", 3, 70, 32, True, 1.0 / math.sqrt(32), (("normal", 0.0, 2.0),) * 3, seed=6),
+    Workload("h_pat", 2, 64, 64, True, 0.125, REFERENCE_FILLS),
+] + reference_smoke_cases(), ids=lambda w: w.name)
+def test_f64_reference_matches_oracle(wl):
+    q, k, v = wl.make_inputs()
+    ref = fc.oracle(wl, q, k, v, o_init=np.zeros(wl.length("o"), np.float32))
+    mine = fh.attention_f64(wl, q, k, v)
+    idx = fc.active_index(wl)
+    assert np.max(np.abs(mine[idx] - ref[idx])) < 2e-5
+    pad = np.setdiff1d(np.arange(wl.length("o")), idx)
+    assert np.all(mine[pad] == 0)
+
+
+def test_f64_reference_row_subset():
+    wl = Workload("h_rows", 2, 300, 32, True, 0.2, (("normal", 0.0, 1.0),) * 3, seed=9)
+    q, k, v = wl.make_inputs()
+    rows = np.array([0, 1, 17, 150, 299])
+    full = fh.attention_f64(wl, q, k, v)
+    sub = fh.attention_f64(wl, q, k, v, rows)
+    idx = fh.active_index(wl, rows)
+    assert np.array_equal(full[idx], sub[idx])
+
+
+def test_shape_name_and_work_follow_the_reference():
+    assert fh.shape_name(8, 1024, 64, True) == "batch_heads=8,seq=1024,head=64,causal=true"
+    assert fh.shape_name(2, 32, 16, False) == "batch_heads=2,seq=32,head=16,causal=false"
+    # src/main.zig:1032-1034: S(S+1)/2 pairs when causal; Q, K, V f16 + O f32
+    assert fh.reference_work(8, 1024, 64, True) == (1074790400, 8 * 1024 * 64 * 10)
+    assert fh.reference_work(2, 32, 16, False) == (2 * 4 * 32 * 32 * 16, 2 * 32 * 16 * 10)
+
+
+def test_record_fields_and_formulas():
+    rec = fh.make_record("not_cute", "batch_heads=2,seq=32,head=16,causal=false", True, 0.5, 0.4, 0.7,
+                         1_000_000, 2_000_000_000, 1e-4)
+    assert tuple(rec) == fh.RECORD_KEYS
+    assert rec["gbps"] == pytest.approx(1_000_000 / (0.5 * 1e6))         # src/benchmark.zig:83-85
+    assert rec["tflops"] == pytest.approx(2_000_000_000 / (0.5 * 1e9))   # src/benchmark.zig:86-88
+    buf = io.StringIO()
+    fh.emit(rec, buf)
+    line = buf.getvalue()
+    assert line.startswith('{"kernel":"flash_attention","implementation":"not_cute","shape":')
+    assert json.loads(line) == rec
+
+
+def test_compare_table_and_reader():
+    mine = fh.make_record("not_cute", "s1", True, 0.010, 0.009, 0.012, 1, 1, 0.0)
+    base = fh.make_record("torch_sdpa_flash", "s1", True, 0.030, 0.029, 0.031, 1, 1, 0.001)
+    bad = fh.make_record("torch_sdpa_mem_efficient", "s1", False, 0.020, 0.02, 0.02, 1, 1, 0.5)
+    lines = [json.dumps(mine), "not json", "{broken", json.dumps(base), json.dumps(bad), json.dumps({"x": 1})]
+    recs = fh.read_records(lines)
+    assert len(recs) == 3
+    table = fh.compare_table(recs).splitlines()
+    flash_row = [r for r in table if "torch_sdpa_flash" in r][0]
+    assert "3.00x" in flash_row and flash_row.rstrip().endswith("yes")
+    assert [r for r in table if "mem_efficient" in r][0].rstrip().endswith("no")
+
+
+def test_compare_table_cli(tmp_path, capsys):
+    p = tmp_path / "recs.jsonl"
+    p.write_text(json.dumps(fh.make_record("not_cute", "s", True, 1.0, 1.0, 1.0, 1, 1, 0.0)) + "\n" +
+                 json.dumps(fh.make_record("torch_sdpa_math_f32", "s", True, 4.0, 4.0, 4.0, 1, 1, 0.0)) + "\n")
+    assert fh.main(["compare-table", str(p)]) == 0
+    assert "4.00x" in capsys.readouterr().out
+
+
+def test_benchmark_fills():
+    # src/main.zig:787-795: ((i*mul + add) % mod) * scale
+    q = fh.modular_fill(12, 3, 1, 11, 0.125).view(np.float16).astype(np.float32)
+    assert q.tolist() == [((3 * i + 1) % 11) * 0.125 for i in range(12)]
+    v = fh.modular_fill(20, 7, 3, 17, 0.03125).view(np.float16).astype(np.float32)
+    assert v.tolist() == [((7 * i + 3) % 17) * 0.03125 for i in range(20)]

@@ -1,0 +1,69 @@
+"""GPU runs of the flash harness commands (not-cute-zig_amd/flash_harness.py) through the C ABI."""
+
+import json
+
+import pytest
+
+import flash_harness as fh
+import notcute_flash as nc
+
+pytestmark = pytest.mark.gpu
+
+
+def _records(text):
+    return [json.loads(line) for line in text.splitlines() if line.startswith("{")]
+
+
+def test_flash_command(gpu, capsys):
+    """runFlashAttention's four cases (src/main.zig:189-194) within 0.008, pads untouched."""
+    assert fh.main(["flash"]) == 0
+    assert capsys.readouterr().err.count("flash attention OK") == 4
+
+
+def test_compare_command_reference_shapes(gpu, capsys):
+    """runCompareDemo's 15 flash shapes (src/main.zig:141-170): one record each, max-abs <= 0.02."""
+    assert fh.main(["compare", "--warmup", "2", "--iters", "3"]) == 0
+    recs = _records(capsys.readouterr().out)
+    assert len(recs) == 15
+    for r in recs:
+        assert tuple(r) == fh.RECORD_KEYS
+        assert r["implementation"] == "not_cute" and r["correct"] and r["max_abs_error"] <= 0.02
+        assert 0 < r["min_ms"] <= r["mean_ms"] <= r["max_ms"]
+
+
+def test_profile_flash_command(gpu, capsys):
+    """runProfileFlash (src/main.zig:81-130): attributes, occupancy limits, then the c3 compare record."""
+    assert fh.main(["profile-flash", "--warmup", "1", "--iters", "2"]) == 0
+    out = capsys.readouterr().out
+    prof = [json.loads(line)["profile"] for line in out.splitlines() if line.startswith('{"profile"')][0]
+    sel = nc.select_kernel(nc.options(batch_heads=8, seq_len=1024, head_dim=64, scale=0.125, causal=True))
+    assert prof["kernel"] == sel.name.decode()
+    assert prof["blocks_per_cu"] >= 1 and prof["waves_per_cu"] == prof["blocks_per_cu"] * sel.threads // 64
+    assert prof["static_lds"] == sel.lds_bytes and prof["local"] == 0
+    assert prof["cu_count"] >= 1 and prof["device"].startswith("gfx950")
+    rec = _records(out)[-1]
+    assert rec["shape"] == "batch_heads=8,seq=1024,head=64,causal=true" and rec["correct"]
+
+
+def test_benchmark_flash_command(gpu, capsys):
+    assert fh.main(["benchmark-flash", "--warmup", "1", "--iters", "2"]) == 0
+    out = capsys.readouterr().out
+    assert out.count("--- Benchmark:") == 5 and out.count("TFLOPs") == 5
+
+
+def test_baselines_command_in_own_process(gpu):
+    """torch SDPA records for the first reference shapes, from a child process (PyTorch brings its
+    own HIP runtime); each record carries the reference's fields and a max-abs error."""
+    import os
+    import subprocess
+    import sys
+
+    harness = os.path.join(os.path.dirname(fh.__file__), "flash_harness.py")
+    r = subprocess.run([sys.executable, harness, "baselines", "--limit", "3", "--warmup", "1", "--iters", "2"],
+                       capture_output=True, text=True, timeout=300)
+    print(r.stderr[-2000:])
+    assert r.returncode == 0
+    recs = _records(r.stdout)
+    assert recs and all(tuple(x) == fh.RECORD_KEYS for x in recs)
+    assert {x["implementation"] for x in recs} <= set(fh.BASELINE_IMPLS)
+    assert any(x["implementation"] == "torch_sdpa_math_f32" and x["correct"] for x in recs)
