@@ -881,6 +881,155 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Reference-ABI entry points: the kernel symbols the reference's code object exports
+// (flash_attention_fwd_{v2,opt,h64,h64_bn32,h64_causal} and the legacy flash_attention_fwd,
+// src/main_device.zig:19-47) with their parameter list (q, k, v, o, seq_len, head_dim,
+// q/k/v/o_stride, scale, causal; 88 bytes) and launch geometry: grid (ceil(S/16), batch_heads),
+// block = the reference's thread count (64 or 128: one or two waves), rows of exactly head_dim
+// elements, any slice stride and base alignment. They exist so callers that look kernels up by
+// the reference's names (src/main.zig:822-828, 1024-1030) keep working; nc_flash_launch with the
+// gfx950 dispatch is the fast path.
+//
+// Workgroup (bx, by): query rows 16bx .. 16bx+15 of slice by. Every wave computes those 16 rows
+// over every NW-th 32-key chunk with 16x16x32 MFMAs in the transposed form (S^T = K Q^T,
+// O^T += V^T P^T); operands are gathered element by element from global memory (no alignment
+// assumed), the softmax takes each chunk's max after scaling (any sign of scale), and the waves'
+// partials merge through LDS. Lane l holds query l%16; in S^T tile t it holds keys 16t+4(l/16)+r,
+// and those 8 keys are, in order, its k-values of the P^T and V^T operands.
+// ---------------------------------------------------------------------------------------------
+constexpr int kRefMaxWaves = 4;
+
+template <int D>
+__device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                                      float *o, int S, uint64_t q_stride, uint64_t k_stride,
+                                                      uint64_t v_stride, uint64_t o_stride, float scale,
+                                                      bool causal, char *smem) {
+    constexpr int DH = (D + 31) / 32;  // 32-column k-steps of S^T
+    constexpr int DT = D / 16;         // 16-row O^T tiles
+    constexpr int OP = D + 4;
+    const int NW = (int)(blockDim.x >> 6);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+    const int r0 = 16 * (int)blockIdx.x;
+    const size_t head = blockIdx.y;
+    if (r0 >= S) return;
+    const uint16_t *qh = q + head * q_stride, *kh = k + head * k_stride, *vh = v + head * v_stride;
+    float *oh = o + head * o_stride;
+    const int qrow = r0 + c;
+    const int lim_row = causal ? min(qrow, S - 1) : S - 1;  // last key visible to this lane's query
+    const int kv_end = causal ? min(S, r0 + 16) : S;
+    const int nch = (kv_end + 31) >> 5;
+
+    auto gather8 = [&](const uint16_t *base, int row, int d0) {  // 8 f16 of one row, zero outside
+        half8 x = {};
+        if (row < S) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (d0 + j < D) x[j] = __builtin_bit_cast(_Float16, base[(size_t)row * D + d0 + j]);
+        }
+        return x;
+    };
+    half8 qf[DH];
+#pragma unroll
+    for (int h = 0; h < DH; ++h) qf[h] = gather8(qh, qrow, 32 * h + 8 * g);
+
+    const float sc = scale * kLog2e;
+    float mrow = neg_inf(), l = 0.f;
+    floatx4 oacc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] = floatx4{};
+    const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+    for (int ch = w; ch < nch; ch += NW) {
+        const int kt0 = 32 * ch;
+        floatx4 s[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = floatx4{};
+#pragma unroll
+            for (int h = 0; h < DH; ++h)
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(gather8(kh, kt0 + 16 * t + c, 32 * h + 8 * g), qf[h], s[t], 0, 0, 0);
+        }
+        float x[8];
+        float lm = neg_inf();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int key = kt0 + 16 * (e >> 2) + 4 * g + (e & 3);
+            x[e] = key > lim_row ? neg_inf() : s[e >> 2][e & 3] * sc;
+            lm = fmaxf(lm, x[e]);
+        }
+        lm = fmaxf(lm, __shfl_xor(lm, 16));
+        lm = fmaxf(lm, __shfl_xor(lm, 32));
+        const float m_new = fmaxf(mrow, lm);
+        const float m_use = m_new == neg_inf() ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(mrow - m_use);
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        mrow = m_new;
+        half8 pb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[e] = (_Float16)__builtin_amdgcn_exp2f(x[e] - m_use);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const half2v hp = {pb[2 * t], pb[2 * t + 1]};
+            l = __builtin_amdgcn_fdot2(hp, ones, l, false);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            half8 va = {};
+            const int d = 16 * dt + c;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int key = kt0 + 16 * (e >> 2) + 4 * g + (e & 3);
+                if (key < S) va[e] = __builtin_bit_cast(_Float16, vh[(size_t)key * D + d]);
+            }
+            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, oacc[dt], 0, 0, 0);
+        }
+    }
+
+    // Merge the waves' partials: per-query (m, l) and scaled O^T through LDS.
+    float lt = l + __shfl_xor(l, 16);
+    lt += __shfl_xor(lt, 32);
+    float2v *mlb = reinterpret_cast<float2v *>(smem);                              // [NW][16]
+    float *ob = reinterpret_cast<float *>(smem + kRefMaxWaves * 16 * sizeof(float2v));  // [NW][16][OP]
+    if (g == 0) mlb[w * 16 + c] = float2v{mrow, lt};
+    __syncthreads();
+    float mmax = neg_inf(), den = 0.f;
+    for (int j = 0; j < NW; ++j) mmax = fmaxf(mmax, mlb[j * 16 + c][0]);
+    for (int j = 0; j < NW; ++j) den += __builtin_amdgcn_exp2f(mlb[j * 16 + c][0] - mmax) * mlb[j * 16 + c][1];
+    const float wgt = __builtin_amdgcn_exp2f(mrow - mmax) / den;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ob[(w * 16 + c) * OP + 16 * dt + 4 * g + r] = oacc[dt][r] * wgt;
+    __syncthreads();
+    for (int u = threadIdx.x; u < 16 * D; u += blockDim.x) {
+        const int qi = u / D, d = u % D;
+        if (r0 + qi >= S) continue;
+        float acc = 0.f;
+        for (int j = 0; j < NW; ++j) acc += ob[(j * 16 + qi) * OP + d];
+        oh[(size_t)(r0 + qi) * D + d] = acc;
+    }
+}
+
+__device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o,
+                                                 uint64_t seq_len, uint64_t head_dim, uint64_t q_stride,
+                                                 uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, float scale,
+                                                 uint32_t causal) {
+    __shared__ __attribute__((aligned(16))) char smem[kRefMaxWaves * 16 * (8 + (64 + 4) * 4)];
+    // Shapes the reference's kernels reject return without writing (src/flash_h64_bn32.zig:40).
+    if (seq_len == 0 || seq_len > 0x7fffffffull || (blockDim.x & 63) || blockDim.x > 64 * kRefMaxWaves) return;
+    const int S = (int)seq_len;
+    if (head_dim == 16)
+        flash_fwd_refabi_body<16>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, causal != 0, smem);
+    else if (head_dim == 32)
+        flash_fwd_refabi_body<32>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, causal != 0, smem);
+    else if (head_dim == 64)
+        flash_fwd_refabi_body<64>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, causal != 0, smem);
+}
+
 }  // namespace
 
 #define NC_FLASH_KERNEL(NAME, D, NQ, NS, CAUSAL, VEC)                                   \
@@ -943,3 +1092,19 @@ NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_causal, 16, 2, 4, true, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_full, 16, 1, 8, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_causal, 16, 1, 8, true, 2, 1)
 
+// Reference-ABI symbols (src/flash_v2.zig:23, src/flash_opt.zig:17, src/flash_h64.zig:21,
+// src/flash_h64_bn32.zig:26, src/flash_h64_causal.zig:20, src/kernels.zig:380): one body, launched
+// with the reference's grid (ceil(S/16), batch_heads) and 64 or 128 threads.
+#define NC_FLASH_REFABI_KERNEL(NAME)                                                                  \
+    extern "C" __global__ __launch_bounds__(256) void NAME(                                           \
+        const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t seq_len,          \
+        uint64_t head_dim, uint64_t q_stride, uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, \
+        float scale, uint32_t causal) {                                                               \
+        flash_fwd_refabi(q, k, v, o, seq_len, head_dim, q_stride, k_stride, v_stride, o_stride, scale, causal); \
+    }
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_v2)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_opt)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_bn32)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_causal)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd)

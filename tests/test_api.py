@@ -281,3 +281,15 @@ def test_seeded_fills():
     assert np.array_equal(nc.fill_normal(1000, 3, 1), nc.fill_normal(5000, 3, 1)[:1000])
     assert not np.array_equal(nc.fill_normal(1000, 3, 1), nc.fill_normal(1000, 3, 2))
     assert not np.array_equal(nc.fill_uniform(1000, 3, 1), nc.fill_uniform(1000, 4, 1))
+
+
+def test_code_object_exports_reference_kernel_symbols():
+    """The gfx950 code object carries the reference's kernel names (src/main_device.zig:19-47) next to
+    its own, so callers that look kernels up by those names keep working."""
+    import os
+    path = os.path.join(os.path.dirname(__file__), "..", "not-cute-zig_amd", "flash_fwd_gfx950.hsaco")
+    blob = open(path, "rb").read()
+    for name in ("flash_attention_fwd_v2", "flash_attention_fwd_opt", "flash_attention_fwd_h64",
+                 "flash_attention_fwd_h64_bn32", "flash_attention_fwd_h64_causal"):
+        assert name.encode() + b"\0" in blob, name
+    assert b"\0flash_attention_fwd\0" in blob
