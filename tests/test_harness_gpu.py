@@ -28,7 +28,8 @@ def test_compare_command_reference_shapes(gpu, capsys):
     for r in recs:
         assert tuple(r) == fh.RECORD_KEYS
         assert r["implementation"] == "not_cute" and r["correct"] and r["max_abs_error"] <= 0.02
-        assert 0 < r["min_ms"] <= r["mean_ms"] <= r["max_ms"]
+        # mean/min/max are f32 in the C result (BenchmarkResult), so allow one rounding step
+        assert 0 < r["min_ms"] <= r["mean_ms"] * (1 + 1e-6) and r["mean_ms"] <= r["max_ms"] * (1 + 1e-6)
 
 
 def test_profile_flash_command(gpu, capsys):
