@@ -104,14 +104,28 @@ const char *reference_kernel(const nc_flash_options &o) {
 // they are preferred while the grid still gives every CU at least one workgroup; short or few
 // sequences move to narrower query blocks whose keys are split over more waves, so that even the
 // heaviest (causal: last) query block finishes in a few key-block steps.
+// Chosen from GPU sweeps of every variant over BH x S x d x causal (48 + 42 shapes). The shared-
+// staging kernels (q8s1, q4s1, q2s4) need enough workgroups to fill the CUs twice over; causal
+// masking makes their per-workgroup work uneven, so they need more of them (or short sequences)
+// before they beat the private-staging q1s8, whose 8 key-split waves stay balanced on any grid.
 const Variant *choose_pipe(const nc_flash_options &o) {
-    constexpr uint64_t kCUs = 256;
     const uint32_t d = (uint32_t)o.head_dim;
     const bool causal = o.causal != 0;
-    auto wgs = [&](uint64_t bm) { return ((o.seq_len + bm - 1) / bm) * o.batch_heads; };
-    if (d == 64 && wgs(256) >= kCUs) return find_pipe(d, 8, 1, causal);
-    if (d >= 32 && wgs(128) >= kCUs) return find_pipe(d, 4, 1, causal);
-    if (wgs(64) >= kCUs) return find_pipe(d, 2, 4, causal);
+    const uint64_t S = o.seq_len;
+    auto wgs = [&](uint64_t bm) { return ((S + bm - 1) / bm) * o.batch_heads; };
+    if (d == 64) {
+        if (causal && S <= 512 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal);
+        if (causal ? (wgs(256) >= 512 || (wgs(256) >= 256 && S <= 1024)) : wgs(256) >= 256)
+            return find_pipe(d, 8, 1, causal);
+        if (wgs(64) >= 256 && (!causal || o.batch_heads >= 2)) return find_pipe(d, 2, 4, causal);
+        return find_pipe(d, 1, 8, causal);
+    }
+    if (d == 32) {
+        if ((S <= 512 && wgs(128) >= 512) || (S <= 1024 && wgs(128) >= 1024)) return find_pipe(d, 4, 1, causal);
+        if (wgs(64) >= (causal ? 1024u : 512u)) return find_pipe(d, 2, 4, causal);
+        return find_pipe(d, 1, 8, causal);
+    }
+    if (wgs(64) >= 1024) return find_pipe(d, 2, 4, causal);
     return find_pipe(d, 1, 8, causal);
 }
 
