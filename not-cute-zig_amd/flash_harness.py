@@ -6,6 +6,7 @@ runner (modal_run.py:34-69), on one MI355X through the C ABI.
     python flash_harness.py flash                 # runFlashAttention's four cases (src/main.zig:189-194)
     python flash_harness.py compare               # runCompareDemo's flash shapes as JSONL (src/main.zig:141-170)
     python flash_harness.py baselines             # PyTorch SDPA on the same shapes (tools/pytorch_baselines.py)
+    python flash_harness.py materialized          # rocBLAS QK^T -> softmax -> PV (tools/cuda_baselines.cu:689-759)
     python flash_harness.py profile-flash         # runProfileFlash (src/main.zig:81-130)
     python flash_harness.py benchmark-flash       # runFlashBenchmark (src/main.zig:760-766)
     python flash_harness.py compare-table FILE... # the baseline-vs-not-cute table (modal_run.py:34-69)
@@ -294,6 +295,69 @@ def cmd_baselines(args) -> int:
     return 0 if n else 1
 
 
+def materialized_record(plan: nc.Materialized, stream: nc.Stream, wl: Workload, q, k, v,
+                        rows: Optional[np.ndarray], warmup: int, iters: int) -> Dict:
+    """One `cublas_materialized` record (tools/cuda_baselines.cu:744-759): the output checked against
+    the float64 reference, per-call event timing, bytes = inputs + output + workspace."""
+    shape = shape_name(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
+    flops, bytes_ = reference_work(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
+    opts = wl.options()
+    ws_bytes = nc.Materialized.workspace_bytes(opts)
+    bufs = [nc.DeviceBuffer.from_array(x) for x in (q, k, v)]
+    bufs.append(nc.DeviceBuffer.from_array(np.zeros(wl.length("o"), np.float32)))
+    bufs.append(nc.DeviceBuffer(ws_bytes))
+    e0, e1 = nc.Event(), nc.Event()
+    try:
+        def run():
+            plan.run(*bufs[:4], bufs[4], opts)
+
+        run()
+        stream.synchronize()
+        out = bufs[3].download(np.float32, wl.length("o"))
+        for _ in range(warmup):
+            run()
+        stream.synchronize()
+        samples = []
+        for _ in range(iters):
+            e0.record(stream.handle)
+            run()
+            e1.record(stream.handle)
+            e1.synchronize()
+            samples.append(nc.Event.elapsed(e0, e1))
+    finally:
+        e0.destroy()
+        e1.destroy()
+        for b in bufs:
+            b.free()
+    ref = attention_f64(wl, q, k, v, rows)
+    idx = np.arange(wl.length("o")) if rows is None else active_index(wl, rows)
+    err = float(np.max(np.abs(out[idx] - ref[idx])))
+    rec = make_record("rocblas_materialized", shape, err <= BASELINE_TOL, sum(samples) / len(samples),
+                      min(samples), max(samples), bytes_ + ws_bytes, flops, err)
+    rec["workspace_bytes"] = ws_bytes
+    return rec
+
+
+def cmd_materialized(_module: nc.Module, args) -> int:
+    """tools/cuda_baselines.cu:689-759 over the `compare` shapes and inputs, in this process."""
+    cases = compare_workloads(args.shapes)
+    if args.limit:
+        cases = cases[:args.limit]
+    stream = nc.Stream()
+    plan = nc.Materialized(stream.handle)
+    status = 0
+    try:
+        for wl, rows in cases:
+            q, k, v = wl.make_inputs()
+            rec = materialized_record(plan, stream, wl, q, k, v, rows, args.warmup, args.iters)
+            status |= 0 if rec["correct"] else 1
+            emit(rec)
+    finally:
+        plan.destroy()
+        stream.destroy()
+    return status
+
+
 # ---------------------------------------------------------------------------------------------
 # profile-flash: runProfileFlash (src/main.zig:81-130)
 # ---------------------------------------------------------------------------------------------
@@ -384,7 +448,7 @@ def cmd_benchmark(module: nc.Module, args) -> int:
 # ---------------------------------------------------------------------------------------------
 
 BASELINE_IMPLS = ("torch_sdpa_flash", "torch_sdpa_mem_efficient", "torch_sdpa_math", "torch_sdpa_math_f32",
-                  "cublas_materialized", "cuda_wmma", "cuda_tiled")
+                  "rocblas_materialized", "cublas_materialized", "cuda_wmma", "cuda_tiled")
 
 
 def read_records(lines: Iterable[str]) -> List[Dict]:
@@ -442,7 +506,10 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     b = sub.add_parser("baselines", help="torch SDPA records for the compare shapes (JSONL on stdout)")
     b.add_argument("--shapes", choices=("reference", "configs"), default="reference")
     b.add_argument("--limit", type=int, default=0, help="only the first N shapes")
-    for q in (p, b, sub.add_parser("profile-flash", help="attributes and occupancy of the c3 kernel"),
+    m = sub.add_parser("materialized", help="rocBLAS materialized-attention records for the compare shapes")
+    m.add_argument("--shapes", choices=("reference", "configs"), default="reference")
+    m.add_argument("--limit", type=int, default=0, help="only the first N shapes")
+    for q in (p, b, m, sub.add_parser("profile-flash", help="attributes and occupancy of the c3 kernel"),
               sub.add_parser("benchmark-flash", help="runFlashBenchmark's five cases")):
         q.add_argument("--warmup", type=int, default=5)
         q.add_argument("--iters", type=int, default=20)
@@ -456,7 +523,7 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     nc.init()
     module = nc.Module.load_embedded()
     return {"flash": cmd_flash, "compare": cmd_compare, "profile-flash": cmd_profile,
-            "benchmark-flash": cmd_benchmark}[args.cmd](module, args)
+            "benchmark-flash": cmd_benchmark, "materialized": cmd_materialized}[args.cmd](module, args)
 
 
 if __name__ == "__main__":

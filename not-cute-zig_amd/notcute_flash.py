@@ -604,3 +604,73 @@ def f32_to_f16(x: float) -> int:
 
 def f16_to_f32(h: int) -> float:
     return float(lib().nc_f16_to_f32(h))
+
+
+# ---------------------------------------------------------------------------------------------
+# Materialized-attention baseline (include/notcute_baselines.h, libnotcute_baselines.so):
+# the cublas_materialized case of tools/cuda_baselines.cu:689-759 with rocBLAS GEMMs.
+# ---------------------------------------------------------------------------------------------
+
+BASELINES_PATH = os.path.join(HERE, "libnotcute_baselines.so")
+MATERIALIZED_MAX_SEQ = 32768
+_BASE_SIGS = {
+    "nc_materialized_create": (ctypes.c_int, [ctypes.POINTER(_P), _P]),
+    "nc_materialized_destroy": (ctypes.c_int, [_P]),
+    "nc_materialized_workspace_bytes": (_U64, [ctypes.POINTER(FlashOptions)]),
+    "nc_materialized_attention": (
+        ctypes.c_int,
+        [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, _U64,
+         ctypes.POINTER(FlashOptions)]),
+    "nc_materialized_last_error": (ctypes.c_char_p, []),
+}
+_blib: Optional[ctypes.CDLL] = None
+
+
+def baselines_library(path: str = BASELINES_PATH) -> ctypes.CDLL:
+    """Load libnotcute_baselines.so (after libnotcute_flash.so, which it links); raises if unbuilt."""
+    global _blib
+    if _blib is not None:
+        return _blib
+    load_library()
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run `make -C not-cute-zig_amd` or __graft_entry__.build() first")
+    b = ctypes.CDLL(path)
+    for name, (res, args) in _BASE_SIGS.items():
+        fn = getattr(b, name)
+        fn.restype = res
+        fn.argtypes = args
+    _blib = b
+    return b
+
+
+def _check_base(status: int, what: str) -> None:
+    if status != 0:
+        detail = (baselines_library().nc_materialized_last_error() or b"").decode(errors="replace")
+        raise NcError(status, what, detail)
+
+
+class Materialized:
+    """QK^T GEMM -> softmax kernel -> PV GEMM on one stream (rocBLAS handle bound to it)."""
+
+    def __init__(self, stream: Optional[int] = None):
+        h = ctypes.c_void_p()
+        _check_base(baselines_library().nc_materialized_create(ctypes.byref(h), stream), "materialized.create")
+        self.handle = int(h.value)
+
+    @staticmethod
+    def workspace_bytes(opts: FlashOptions) -> int:
+        """BH*S*S f32 scores + BH*S*S f16 probabilities; 0 for invalid options."""
+        return int(baselines_library().nc_materialized_workspace_bytes(ctypes.byref(opts)))
+
+    def run(self, q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, o: DeviceBuffer, workspace: DeviceBuffer,
+            opts: FlashOptions, q_len: Optional[int] = None, k_len: Optional[int] = None,
+            v_len: Optional[int] = None, o_len: Optional[int] = None) -> None:
+        _check_base(baselines_library().nc_materialized_attention(
+            self.handle, q.ptr, q.nbytes // 2 if q_len is None else q_len, k.ptr, k.nbytes // 2 if k_len is None else k_len,
+            v.ptr, v.nbytes // 2 if v_len is None else v_len, o.ptr, o.nbytes // 4 if o_len is None else o_len,
+            workspace.ptr, workspace.nbytes, ctypes.byref(opts)), "materialized.attention")
+
+    def destroy(self) -> None:
+        if self.handle:
+            _check_base(baselines_library().nc_materialized_destroy(self.handle), "materialized.destroy")
+            self.handle = 0
