@@ -15,6 +15,7 @@ reference) timed on this host on the same workload.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -49,7 +50,8 @@ def cpu_baseline(wl, q, k, v, budget_s: float) -> dict:
     while True:
         flash_oracle.flash_fwd(q, k, v, o, batch_heads=wl.batch_heads, seq_len=wl.seq_len, head_dim=wl.head_dim,
                                q_stride=wl.stride("q"), k_stride=wl.stride("k"), v_stride=wl.stride("v"),
-                               o_stride=wl.stride("o"), scale=wl.scale, causal=wl.causal, threads=1)
+                               o_stride=wl.stride("o"), scale=wl.scale, causal=wl.causal, threads=1,
+                               dtype=wl.dtype)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
@@ -63,6 +65,18 @@ def cpu_baseline(wl, q, k, v, budget_s: float) -> dict:
         "sample": f"full {wl.name} workload ({wl.describe()}) x {reps} repetitions, {el:.1f} s, one thread, "
                   f"C restatement of src/main.zig:1271-1307 (-O3, no fast-math)",
     }, o
+
+
+def describe_dists(dists) -> str:
+    """'N(0,1)' when Q, K and V share one distribution, else 'Q N(0,3) K N(0,3) V U(-1,1)'."""
+    def one(d):
+        if d[0] == "normal":
+            return f"N({d[1]:g},{d[2]:g})"
+        if d[0] == "uniform":
+            return f"U({d[1]:g},{d[2]:g})"
+        return f"((i*{d[1]}+{d[2]})%17)*{d[3]:g}"
+    names = [one(d) for d in dists]
+    return names[0] if len(set(names)) == 1 else " ".join(f"{t} {n}" for t, n in zip("QKV", names))
 
 
 def calibrate_copy(mod: nc.Module, stream: nc.Stream, nbytes: int, iters: int) -> None:
@@ -95,6 +109,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run the plain copy kernel on MIB MiB (profiling runs only)")
     ap.add_argument("--no-verify", action="store_true", help="skip the oracle check of the output")
+    ap.add_argument("--dtype", choices=("f16", "bf16"), default="f16",
+                    help="element type of Q/K/V (f16: the reference's and the headline's)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -107,6 +123,8 @@ def main() -> int:
             return 2
 
     wl = CONFIGS[args.workload]
+    if args.dtype != wl.dtype:
+        wl = dataclasses.replace(wl, dtype=args.dtype)
     opts = wl.options()
     work = wl.work()
     sel = nc.select_kernel(opts)
@@ -137,7 +155,8 @@ def main() -> int:
         out = do.download(np.float32, wl.length("o"))
         max_abs, max_rel = flashcheck.errors(out, ref, idx)
         log(f"bench: parity vs oracle max-abs {max_abs:.3e} max-rel {max_rel:.3e}")
-        if not (max_abs <= flashcheck.MAX_ABS and max_rel <= flashcheck.MAX_REL):
+        bar_abs, bar_rel = flashcheck.parity_bar(wl.dtype)
+        if not (max_abs <= bar_abs and max_rel <= bar_rel):
             print(json.dumps({"error": "parity failure", "max_abs": max_abs, "max_rel": max_rel}))
             return 1
 
@@ -212,11 +231,12 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": wl.dtype,
         "data": "synthetic",
         "config": {"workload": f"{wl.name}: flash-attn fwd BH={wl.batch_heads} S={wl.seq_len} d={wl.head_dim} "
-                               f"{'causal' if wl.causal else 'non-causal'}, Q/K/V f16 N(0,1) seed {wl.seed}, "
-                               f"scale {wl.scale:g}, f32 accumulate/out",
+                               f"{'causal' if wl.causal else 'non-causal'}, Q/K/V {wl.dtype} "
+                               f"{describe_dists(wl.dists)} seed {wl.seed}, scale {wl.scale:g}, "
+                               f"f32 accumulate/out",
                    "batch_heads": wl.batch_heads, "seq_len": wl.seq_len, "head_dim": wl.head_dim,
                    "causal": wl.causal, "kernel": sel.name.decode(), "parallelism": "single-gpu"},
         "pct_f16_mfma_peak": round(100.0 * tflops / PEAK_F16_TFLOPS, 3),

@@ -10,7 +10,8 @@
  * probability matrices (for causal too, as the reference does).
  *
  * Conventions as in notcute_flash.h: nc_status return codes, plain device pointers, Q/K/V f16 bit
- * patterns, O f32, asynchronous on the plan's stream, one process / one GPU / one calling thread.
+ * patterns (bf16 with element_type NC_ELEMENT_BF16, probabilities then bf16 too), O f32,
+ * asynchronous on the plan's stream, one process / one GPU / one calling thread.
  * Layout and validation are those of nc_flash_options / nc_flash_validate, row strides included.
  * The library links libnotcute_flash.so (validation, status names) and librocblas.so.
  */
@@ -37,7 +38,7 @@ int nc_materialized_create(nc_materialized *out, nc_stream stream);
 /* cublasDestroy (tools/cuda_baselines.cu:760). NULL is accepted. */
 int nc_materialized_destroy(nc_materialized plan);
 
-/* Workspace the caller provides: BH*S*S f32 scores followed by BH*S*S f16 probabilities
+/* Workspace the caller provides: BH*S*S f32 scores followed by BH*S*S 16-bit probabilities
  * (scores_len * (sizeof(float) + sizeof(half)), tools/cuda_baselines.cu:683-686, 757). Returns 0
  * when the options are invalid or the size overflows 64 bits. */
 uint64_t nc_materialized_workspace_bytes(const nc_flash_options *opts);

@@ -170,10 +170,16 @@ int nc_graph_destroy(nc_graph graph);
  * Flash-attention forward (src/flash.zig:5-100).
  * ---------------------------------------------------------------------------------------------- */
 
+/* Element type of Q/K/V (O is always f32). The reference computes in f16 only; bf16 is an
+ * extension served by the `_bf16` kernels. */
+#define NC_ELEMENT_F16 0u
+#define NC_ELEMENT_BF16 1u
+
 /* flash.Options (src/flash.zig:5-14). The first nine fields are the reference's, in order and
  * meaning (element strides between (batch, head) slices). The four row strides are an extension:
  * elements between consecutive rows inside a slice; 0 means head_dim, which is exactly the
- * reference's layout (every reference kernel indexes row*head_dim+col). */
+ * reference's layout (every reference kernel indexes row*head_dim+col). element_type is an
+ * extension too: NC_ELEMENT_F16 (0, the reference's type and the default) or NC_ELEMENT_BF16. */
 typedef struct nc_flash_options {
     uint64_t batch_heads; /* default 1 */
     uint64_t seq_len;
@@ -188,6 +194,7 @@ typedef struct nc_flash_options {
     uint64_t k_row_stride;
     uint64_t v_row_stride;
     uint64_t o_row_stride;
+    uint32_t element_type; /* NC_ELEMENT_F16 (default) or NC_ELEMENT_BF16 */
 } nc_flash_options;
 
 /* Field defaults of flash.Options: batch_heads = 1, causal = false, row strides = head_dim;
@@ -195,8 +202,9 @@ typedef struct nc_flash_options {
 void nc_flash_options_init(nc_flash_options *opts);
 
 /* Options.validate (src/flash.zig:16-28): NC_ERROR_INVALID_VALUE when batch_heads == 0,
- * seq_len == 0, head_dim not in {16,32,64}, a row stride below head_dim, or a slice stride below
- * (seq_len-1)*row_stride + head_dim (= seq_len*head_dim for the reference layout).
+ * seq_len == 0, head_dim not in {16,32,64}, a row stride below head_dim, a slice stride below
+ * (seq_len-1)*row_stride + head_dim (= seq_len*head_dim for the reference layout), or an unknown
+ * element_type.
  * NC_ERROR_OVERFLOW when batch_heads*stride does not fit in 64 bits. */
 int nc_flash_validate(const nc_flash_options *opts);
 
@@ -319,9 +327,15 @@ void nc_fill_flash_input(uint16_t *data, size_t n, uint64_t mul, uint64_t add, f
  * Box-Muller on element pairs; every value rounded to f16 round-to-nearest-even. */
 void nc_fill_uniform_f16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float lo, float hi);
 void nc_fill_normal_f16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float mean, float sigma);
+/* The same draws rounded to bfloat16 (round-to-nearest-even) for the bf16 extension. */
+void nc_fill_uniform_bf16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float lo, float hi);
+void nc_fill_normal_bf16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float mean, float sigma);
 /* IEEE binary16 <-> binary32 (round-to-nearest-even, overflow to inf, subnormals kept). */
 uint16_t nc_f32_to_f16(float x);
 float nc_f16_to_f32(uint16_t h);
+/* bfloat16 (the upper half of a binary32) <-> binary32; rounding to nearest even, NaN kept quiet. */
+uint16_t nc_f32_to_bf16(float x);
+float nc_bf16_to_f32(uint16_t h);
 
 /* Library version string. */
 const char *nc_version(void);

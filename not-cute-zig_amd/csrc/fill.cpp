@@ -90,13 +90,34 @@ void nc_fill_flash_input(uint16_t *data, size_t n, uint64_t mul, uint64_t add, f
     for (size_t i = 0; i < n; ++i) data[i] = nc_f32_to_f16((float)((i * mul + add) % 17) * scale);
 }
 
-void nc_fill_uniform_f16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float lo, float hi) {
-    const uint64_t key = stream_key(seed, tensor_id);
-    const double span = double(hi) - double(lo);
-    for (size_t i = 0; i < n; ++i) out[i] = nc_f32_to_f16((float)(double(lo) + span * unit24(draw(key, i))));
+uint16_t nc_f32_to_bf16(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);  // nan: keep it quiet
+    x += 0x7fffu + ((x >> 16) & 1u);  // round to nearest even (carries into the exponent, up to inf)
+    return (uint16_t)(x >> 16);
 }
 
-void nc_fill_normal_f16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float mean, float sigma) {
+float nc_bf16_to_f32(uint16_t h) {
+    const uint32_t x = uint32_t(h) << 16;
+    float f;
+    std::memcpy(&f, &x, 4);
+    return f;
+}
+
+}  // extern "C"
+
+namespace {
+
+template <uint16_t (*ROUND)(float)>
+void fill_uniform(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float lo, float hi) {
+    const uint64_t key = stream_key(seed, tensor_id);
+    const double span = double(hi) - double(lo);
+    for (size_t i = 0; i < n; ++i) out[i] = ROUND((float)(double(lo) + span * unit24(draw(key, i))));
+}
+
+template <uint16_t (*ROUND)(float)>
+void fill_normal(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float mean, float sigma) {
     const uint64_t key = stream_key(seed, tensor_id);
     const double two_pi = 6.283185307179586476925286766559;
     for (size_t j = 0; 2 * j < n; ++j) {
@@ -104,9 +125,29 @@ void nc_fill_normal_f16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_
         const double u2 = unit24(draw(key, 2 * j + 1));
         const double rad = std::sqrt(-2.0 * std::log(u1));
         const double th = two_pi * u2;
-        out[2 * j] = nc_f32_to_f16((float)(double(mean) + double(sigma) * rad * std::cos(th)));
-        if (2 * j + 1 < n) out[2 * j + 1] = nc_f32_to_f16((float)(double(mean) + double(sigma) * rad * std::sin(th)));
+        out[2 * j] = ROUND((float)(double(mean) + double(sigma) * rad * std::cos(th)));
+        if (2 * j + 1 < n) out[2 * j + 1] = ROUND((float)(double(mean) + double(sigma) * rad * std::sin(th)));
     }
+}
+
+}  // namespace
+
+extern "C" {
+
+void nc_fill_uniform_f16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float lo, float hi) {
+    fill_uniform<nc_f32_to_f16>(out, n, seed, tensor_id, lo, hi);
+}
+
+void nc_fill_normal_f16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float mean, float sigma) {
+    fill_normal<nc_f32_to_f16>(out, n, seed, tensor_id, mean, sigma);
+}
+
+void nc_fill_uniform_bf16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float lo, float hi) {
+    fill_uniform<nc_f32_to_bf16>(out, n, seed, tensor_id, lo, hi);
+}
+
+void nc_fill_normal_bf16(uint16_t *out, size_t n, uint64_t seed, uint32_t tensor_id, float mean, float sigma) {
+    fill_normal<nc_f32_to_bf16>(out, n, seed, tensor_id, mean, sigma);
 }
 
 }  // extern "C"

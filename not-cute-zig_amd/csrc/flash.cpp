@@ -33,6 +33,7 @@ struct Variant {
     bool causal;
     bool aligned;
     Family family;
+    bool bf16;  // the `_bf16` twin of the kernel (bf16 Q/K/V)
 
     uint32_t bm() const { return 32 * nq; }
     uint32_t bn() const { return 32 * ns * sub; }
@@ -50,35 +51,41 @@ struct Variant {
     }
 };
 
-#define PIPE(D, NQ, NS, P, C) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "_" C, D, NQ, NS, P, 1, \
-                               C[0] == 'c', true, Family::kPipe}
-#define GEN(D, C, A, SUF) {"nc_flash_fwd_d" #D "_m64_" C SUF, D, 2, 2, 1, 1, C[0] == 'c', A, Family::kGeneric}
+#define PIPE(D, NQ, NS, P, C, T, BF) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "_" C T, D, NQ, NS, P, 1, \
+                                      C[0] == 'c', true, Family::kPipe, BF}
+#define GEN(D, C, A, SUF, T, BF) {"nc_flash_fwd_d" #D "_m64_" C SUF T, D, 2, 2, 1, 1, C[0] == 'c', A, \
+                                  Family::kGeneric, BF}
+// Every kernel of the family, once per element type (T: name suffix, BF: bf16).
+#define VARIANTS(T, BF)                                                                                         \
+    PIPE(64, 8, 1, 3, "full", T, BF), PIPE(64, 8, 1, 3, "causal", T, BF), PIPE(64, 4, 1, 3, "full", T, BF),     \
+    PIPE(64, 4, 1, 3, "causal", T, BF), PIPE(64, 2, 4, 2, "full", T, BF), PIPE(64, 2, 4, 2, "causal", T, BF),   \
+    PIPE(64, 1, 8, 2, "full", T, BF), PIPE(64, 1, 8, 2, "causal", T, BF), PIPE(32, 4, 1, 3, "full", T, BF),     \
+    PIPE(32, 4, 1, 3, "causal", T, BF), PIPE(32, 2, 4, 2, "full", T, BF), PIPE(32, 2, 4, 2, "causal", T, BF),   \
+    PIPE(32, 1, 8, 2, "full", T, BF), PIPE(32, 1, 8, 2, "causal", T, BF), PIPE(16, 2, 4, 2, "full", T, BF),     \
+    PIPE(16, 2, 4, 2, "causal", T, BF), PIPE(16, 1, 8, 2, "full", T, BF), PIPE(16, 1, 8, 2, "causal", T, BF),   \
+    GEN(16, "full", true, "", T, BF), GEN(16, "causal", true, "", T, BF), GEN(32, "full", true, "", T, BF),     \
+    GEN(32, "causal", true, "", T, BF), GEN(64, "full", true, "", T, BF), GEN(64, "causal", true, "", T, BF),   \
+    GEN(16, "full", false, "_unaligned", T, BF), GEN(16, "causal", false, "_unaligned", T, BF),                \
+    GEN(32, "full", false, "_unaligned", T, BF), GEN(32, "causal", false, "_unaligned", T, BF),                \
+    GEN(64, "full", false, "_unaligned", T, BF), GEN(64, "causal", false, "_unaligned", T, BF)
 
-const Variant kVariants[] = {
-    PIPE(64, 8, 1, 3, "full"), PIPE(64, 8, 1, 3, "causal"), PIPE(64, 4, 1, 3, "full"), PIPE(64, 4, 1, 3, "causal"),
-    PIPE(64, 2, 4, 2, "full"), PIPE(64, 2, 4, 2, "causal"), PIPE(64, 1, 8, 2, "full"), PIPE(64, 1, 8, 2, "causal"),
-    PIPE(32, 4, 1, 3, "full"), PIPE(32, 4, 1, 3, "causal"), PIPE(32, 2, 4, 2, "full"), PIPE(32, 2, 4, 2, "causal"),
-    PIPE(32, 1, 8, 2, "full"), PIPE(32, 1, 8, 2, "causal"),
-    PIPE(16, 2, 4, 2, "full"), PIPE(16, 2, 4, 2, "causal"), PIPE(16, 1, 8, 2, "full"), PIPE(16, 1, 8, 2, "causal"),
-    GEN(16, "full", true, ""), GEN(16, "causal", true, ""), GEN(32, "full", true, ""), GEN(32, "causal", true, ""),
-    GEN(64, "full", true, ""), GEN(64, "causal", true, ""),
-    GEN(16, "full", false, "_unaligned"), GEN(16, "causal", false, "_unaligned"),
-    GEN(32, "full", false, "_unaligned"), GEN(32, "causal", false, "_unaligned"),
-    GEN(64, "full", false, "_unaligned"), GEN(64, "causal", false, "_unaligned"),
-};
+const Variant kVariants[] = {VARIANTS("", false), VARIANTS("_bf16", true)};
+#undef VARIANTS
 #undef PIPE
 #undef GEN
 
-const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal) {
+const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal, bool bf16) {
     for (const auto &v : kVariants)
-        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.sub == 1 && v.causal == causal)
+        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.sub == 1 && v.causal == causal &&
+            v.bf16 == bf16)
             return &v;
     return nullptr;
 }
 
-const Variant *find_generic(uint32_t d, bool causal, bool aligned) {
+const Variant *find_generic(uint32_t d, bool causal, bool aligned, bool bf16) {
     for (const auto &v : kVariants)
-        if (v.family == Family::kGeneric && v.d == d && v.causal == causal && v.aligned == aligned) return &v;
+        if (v.family == Family::kGeneric && v.d == d && v.causal == causal && v.aligned == aligned && v.bf16 == bf16)
+            return &v;
     return nullptr;
 }
 
@@ -108,25 +115,28 @@ const char *reference_kernel(const nc_flash_options &o) {
 // staging kernels (q8s1, q4s1, q2s4) need enough workgroups to fill the CUs twice over; causal
 // masking makes their per-workgroup work uneven, so they need more of them (or short sequences)
 // before they beat the private-staging q1s8, whose 8 key-split waves stay balanced on any grid.
+// The bf16 twins have the same instruction stream (bf16 MFMA, conversion and dot forms instead of
+// the f16 ones) and follow the same rule.
 const Variant *choose_pipe(const nc_flash_options &o) {
     const uint32_t d = (uint32_t)o.head_dim;
     const bool causal = o.causal != 0;
+    const bool bf = o.element_type == NC_ELEMENT_BF16;
     const uint64_t S = o.seq_len;
     auto wgs = [&](uint64_t bm) { return ((S + bm - 1) / bm) * o.batch_heads; };
     if (d == 64) {
-        if (causal && S <= 512 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal);
+        if (causal && S <= 512 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal, bf);
         if (causal ? (wgs(256) >= 512 || (wgs(256) >= 256 && S <= 1024)) : wgs(256) >= 256)
-            return find_pipe(d, 8, 1, causal);
-        if (wgs(64) >= 256 && (!causal || o.batch_heads >= 2)) return find_pipe(d, 2, 4, causal);
-        return find_pipe(d, 1, 8, causal);
+            return find_pipe(d, 8, 1, causal, bf);
+        if (wgs(64) >= 256 && (!causal || o.batch_heads >= 2)) return find_pipe(d, 2, 4, causal, bf);
+        return find_pipe(d, 1, 8, causal, bf);
     }
     if (d == 32) {
-        if ((S <= 512 && wgs(128) >= 512) || (S <= 1024 && wgs(128) >= 1024)) return find_pipe(d, 4, 1, causal);
-        if (wgs(64) >= (causal ? 1024u : 512u)) return find_pipe(d, 2, 4, causal);
-        return find_pipe(d, 1, 8, causal);
+        if ((S <= 512 && wgs(128) >= 512) || (S <= 1024 && wgs(128) >= 1024)) return find_pipe(d, 4, 1, causal, bf);
+        if (wgs(64) >= (causal ? 1024u : 512u)) return find_pipe(d, 2, 4, causal, bf);
+        return find_pipe(d, 1, 8, causal, bf);
     }
-    if (wgs(64) >= 1024) return find_pipe(d, 2, 4, causal);
-    return find_pipe(d, 1, 8, causal);
+    if (wgs(64) >= 1024) return find_pipe(d, 2, 4, causal, bf);
+    return find_pipe(d, 1, 8, causal, bf);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -149,7 +159,9 @@ int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selec
     uint64_t max_row = rows[0] > rows[1] ? rows[0] : rows[1];
     max_row = max_row > rows[2] ? max_row : rows[2];
     const bool offsets_fit = max_row < (1ull << 30) && (o.seq_len + 512) * max_row * 2 < (1ull << 31);
-    const Variant *v = (aligned && offsets_fit) ? choose_pipe(o) : find_generic((uint32_t)d, o.causal != 0, aligned);
+    const Variant *v = (aligned && offsets_fit)
+                           ? choose_pipe(o)
+                           : find_generic((uint32_t)d, o.causal != 0, aligned, o.element_type == NC_ELEMENT_BF16);
     if (!v) return NC_ERROR_NOT_FOUND;
     const uint64_t nqb = (o.seq_len + v->bm() - 1) / v->bm();
     uint64_t grid = 0;
@@ -186,6 +198,7 @@ int nc_flash_validate(const nc_flash_options *opts) {
     const nc_flash_options &o = *opts;
     if (o.batch_heads == 0 || o.seq_len == 0) return NC_ERROR_INVALID_VALUE;                   // :17
     if (o.head_dim != 16 && o.head_dim != 32 && o.head_dim != 64) return NC_ERROR_INVALID_VALUE; // :18
+    if (o.element_type != NC_ELEMENT_F16 && o.element_type != NC_ELEMENT_BF16) return NC_ERROR_INVALID_VALUE;
     const uint64_t d = o.head_dim;
     const uint64_t rows[4] = {row_stride_of(o.q_row_stride, d), row_stride_of(o.k_row_stride, d),
                               row_stride_of(o.v_row_stride, d), row_stride_of(o.o_row_stride, d)};

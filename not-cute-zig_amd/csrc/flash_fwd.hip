@@ -26,6 +26,8 @@
 //     the workgroup's last query are never staged. Heavy (late) query blocks are dispatched first and
 //     workgroups of the same heads are kept on one XCD so their K/V stay in that XCD's L2.
 //   * exp is v_exp_f32 on log2-scaled scores (scale * log2(e) folded into one multiply).
+//   * Every kernel also exists with a `_bf16` suffix: bf16 Q/K/V, probabilities rounded to bf16 for
+//     the PV product, v_mfma_f32_32x32x16_bf16 (an extension; the reference computes in f16 only).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -36,6 +38,8 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
@@ -54,6 +58,47 @@ __device__ __forceinline__ float pair_max(float x) {
 __device__ __forceinline__ float pair_sum(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Element type of Q/K/V and of the probabilities fed to the PV product: f16 (BF = false, the
+// reference's type) or bf16. Operands travel as 16-bit payloads in half8 registers either way;
+// only the MFMA, the f32 -> 16-bit rounding of P and the row-sum dot product differ.
+template <bool BF>
+__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
+    if constexpr (BF)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                       0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// Two weights rounded (to nearest even) to the element type, packed as one dword.
+template <bool BF>
+__device__ __forceinline__ half2v round2(float x, float y) {
+    if constexpr (BF) {
+        const bf16x2 p = {(__bf16)x, (__bf16)y};
+        return __builtin_bit_cast(half2v, p);
+    } else {
+        const half2v p = {(_Float16)x, (_Float16)y};
+        return p;
+    }
+}
+// acc + p.x + p.y, with p in the element type (v_dot2c against 1.0 pairs).
+template <bool BF>
+__device__ __forceinline__ float sum2(half2v p, float acc) {
+    if constexpr (BF) {
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), ones, acc, false);
+    } else {
+        const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(p, ones, acc, false);
+    }
+}
+// A 32-key tile's weight sum (per lane, 16 weights) at or above this moves the running max to the
+// tile max. f16: only an overflowed (infinite) weight does. bf16 has f32's range, so weights are
+// held below 2^20 to keep the f32 row sum and O accumulators far from overflow.
+template <bool BF>
+__device__ __forceinline__ float weight_sum_limit() {
+    return BF ? 1048576.0f : __builtin_inff();
 }
 
 // Position of key kk (block-relative) inside a staged V^T row: swap bits 2 and 3.
@@ -107,7 +152,7 @@ struct Cfg {
     static constexpr int VREG = (VU + NT - 1) / NT;
 };
 
-template <int D, int NQ, int NS, bool CAUSAL, bool VEC>
+template <int D, int NQ, int NS, bool CAUSAL, bool VEC, bool BF>
 __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
     using C = Cfg<D, NQ, NS>;
     __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
@@ -257,7 +302,7 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
             const half8 kf = *reinterpret_cast<const half8 *>(krow + 16 * kk);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], acc, 0, 0, 0);
+            acc = mfma32<BF>(kf, qf[kk], acc);
         }
 
         float p[16];
@@ -295,7 +340,11 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) pf[ks][j] = (_Float16)p[8 * ks + j];
+            for (int j = 0; j < 8; j += 2) {
+                const half2v h = round2<BF>(p[8 * ks + j], p[8 * ks + j + 1]);
+                pf[ks][j] = h[0];
+                pf[ks][j + 1] = h[1];
+            }
 
         // O^T += V^T * P^T.
 #pragma unroll
@@ -304,7 +353,7 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const half8 vf = *reinterpret_cast<const half8 *>(vrow + 16 * ks);
-                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], o[mt], 0, 0, 0);
+                o[mt] = mfma32<BF>(vf, pf[ks], o[mt]);
             }
         }
     }
@@ -539,7 +588,7 @@ struct PipeCfg {
     static constexpr int MT = D < 32 ? 1 : D / 32;
 };
 
-template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB>
+template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB, bool BF>
 __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &a) {
     using C = PipeCfg<D, NQ, NS, NSTAGE, SUB>;
     using SW = Swz<D>;
@@ -706,7 +755,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
 #pragma unroll
             for (int kk = 0; kk < D / 16; ++kk) {
                 kf[j * (D / 16) + kk] = lds_load_b128<ST * C::STAGE + 2 * j * ROW16>(kaddr[kk]);
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[j * (D / 16) + kk], qf[kk], acc[j], 0, 0, 0);
+                acc[j] = mfma32<BF>(kf[j * (D / 16) + kk], qf[kk], acc[j]);
             }
         });
         lds_reads_done(kf);
@@ -748,20 +797,21 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
         half8 pf[SUB][2];
         auto weights = [&]() {
-            const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
             float ls = 0.f;
 #pragma unroll
             for (int j = 0; j < SUB; ++j)
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                    for (int r = 0; r < 8; ++r)
-                        pf[j][ks][r] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][8 * ks + r], sc, neg_m));
+                    half2v h[4];
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const half2v h = {pf[j][ks][2 * t], pf[j][ks][2 * t + 1]};
-                        ls = __builtin_amdgcn_fdot2(h, ones, ls, false);
+                        h[t] = round2<BF>(__builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][8 * ks + 2 * t], sc, neg_m)),
+                                          __builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][8 * ks + 2 * t + 1], sc, neg_m)));
+                        pf[j][ks][2 * t] = h[t][0];
+                        pf[j][ks][2 * t + 1] = h[t][1];
                     }
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) ls = sum2<BF>(h[t], ls);
                 }
             return ls;
         };
@@ -790,8 +840,8 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             ls = weights();
         } else {
             ls = weights();
-            if (__builtin_amdgcn_ballot_w64(!(ls < __builtin_inff()))) {
-                to_tile_max();  // a weight overflowed f16: redo the tile against the new max
+            if (__builtin_amdgcn_ballot_w64(!(ls < weight_sum_limit<BF>()))) {
+                to_tile_max();  // a weight overflowed (f16) or grew too large (bf16): redo the tile
                 ls = weights();
             }
         }
@@ -807,7 +857,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 for (int ks = 0; ks < 2; ++ks) {
                     const u32x2 *v4 = vt + (j * C::MT + mt) * 4 + 2 * ks;
                     const u32x4 vv = {v4[0][0], v4[0][1], v4[1][0], v4[1][1]};
-                    o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, vv), pf[j][ks], o[mt], 0, 0, 0);
+                    o[mt] = mfma32<BF>(__builtin_bit_cast(half8, vv), pf[j][ks], o[mt]);
                 }
         __builtin_amdgcn_s_setprio(0);
     };
@@ -1038,9 +1088,13 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
 
 }  // namespace
 
-#define NC_FLASH_KERNEL(NAME, D, NQ, NS, CAUSAL, VEC)                                   \
-    extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) { \
-        flash_fwd_body<D, NQ, NS, CAUSAL, VEC>(a);                                      \
+// Each instantiation defines NAME (f16) and NAME_bf16.
+#define NC_FLASH_KERNEL(NAME, D, NQ, NS, CAUSAL, VEC)                                          \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) {        \
+        flash_fwd_body<D, NQ, NS, CAUSAL, VEC, false>(a);                                      \
+    }                                                                                          \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME##_bf16(nc_flash_kernel_args a) { \
+        flash_fwd_body<D, NQ, NS, CAUSAL, VEC, true>(a);                                       \
     }
 
 // Generic variants (64-bit addressing, register staging): 16-byte aligned rows whose slices are
@@ -1066,16 +1120,24 @@ extern "C" __global__ __launch_bounds__(256) void nc_util_copy_b128(const u32x4 
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256ull) dst[i] = src[i];
 }
 
-#define NC_FLASH_PIPE_KERNEL(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB)                      \
-    extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) { \
-        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB>(a);                         \
+// Each instantiation defines NAME (f16) and NAME_bf16.
+#define NC_FLASH_PIPE_KERNEL(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB)                              \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) {        \
+        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, false>(a);                         \
+    }                                                                                          \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME##_bf16(nc_flash_kernel_args a) { \
+        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, true>(a);                          \
     }
 // With a register budget held to WPE waves per SIMD (512 / WPE VGPRs per wave): two 8-wave
 // workgroups of the 70 KB-LDS variants share a CU only if each wave fits in 128 VGPRs.
-#define NC_FLASH_PIPE_KERNEL_WPE(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB, WPE)                         \
-    extern "C" __global__ __launch_bounds__(NQ * NS * 64) __attribute__((amdgpu_waves_per_eu(WPE))) \
-    void NAME(nc_flash_kernel_args a) {                                                             \
-        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB>(a);                                     \
+#define NC_FLASH_PIPE_KERNEL_WPE(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB, WPE)                             \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) __attribute__((amdgpu_waves_per_eu(WPE)))     \
+    void NAME(nc_flash_kernel_args a) {                                                                 \
+        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, false>(a);                                  \
+    }                                                                                                   \
+    extern "C" __global__ __launch_bounds__(NQ * NS * 64) __attribute__((amdgpu_waves_per_eu(WPE)))     \
+    void NAME##_bf16(nc_flash_kernel_args a) {                                                          \
+        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, true>(a);                                   \
     }
 
 // Pipelined variants: q = query waves (32 rows each), s = key-split waves, p = LDS ring depth.

@@ -8,7 +8,8 @@
 //   O[b][q][c]        = sum_key probs[b][q][key] V[b][key][c]               (f32)
 //
 // Both GEMMs run over the full S x S matrices, causal or not, as the reference's do. This is a
-// baseline to time the fused flash path against; the flash path itself never calls it.
+// baseline to time the fused flash path against; the flash path itself never calls it. With
+// element_type NC_ELEMENT_BF16 the inputs and probabilities are bf16 instead of f16.
 
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
@@ -78,15 +79,31 @@ __device__ float block_reduce(float v, float *red) {
     return v;
 }
 
-template <int NV>
+// Round to the probability type (f16, or bf16 when BF) and back to f32.
+template <bool BF>
+__device__ float round_elem(float x) {
+    if constexpr (BF)
+        return (float)(__bf16)x;
+    else
+        return (float)(_Float16)x;
+}
+template <bool BF>
+__device__ uint16_t elem_bits(float x) {
+    if constexpr (BF)
+        return __builtin_bit_cast(uint16_t, (__bf16)x);
+    else
+        return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+template <int NV, bool BF>
 __global__ __launch_bounds__(1024) void nc_materialized_softmax(const float *__restrict__ scores,
-                                                                 _Float16 *__restrict__ probs, uint32_t S,
+                                                                 uint16_t *__restrict__ probs, uint32_t S,
                                                                  float scale, uint32_t causal) {
     __shared__ float red[16];
     const uint32_t row = blockIdx.x % S;
     const size_t base = (size_t)blockIdx.x * S;  // (slice * S + row) * S
     const float *src = scores + base;
-    _Float16 *dst = probs + base;
+    uint16_t *dst = probs + base;
     const uint32_t T = blockDim.x;
     const uint32_t last = causal ? row : S - 1;  // last visible key
 
@@ -111,8 +128,8 @@ __global__ __launch_bounds__(1024) void nc_materialized_softmax(const float *__r
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const uint32_t j = threadIdx.x + i * T;
-        // The weight is rounded to f16 before it is normalised, and again after.
-        if (j < S) dst[j] = (_Float16)((float)(_Float16)x[i] * inv);
+        // The weight is rounded to the probability type before it is normalised, and again after.
+        if (j < S) dst[j] = elem_bits<BF>(round_elem<BF>(x[i]) * inv);
     }
 }
 
@@ -127,21 +144,28 @@ int softmax_geometry(uint32_t S, uint32_t *threads) {
     return nv;
 }
 
-hipError_t launch_softmax(const float *scores, _Float16 *probs, uint32_t S, uint32_t bh, float scale,
-                          uint32_t causal, hipStream_t stream) {
+template <bool BF>
+hipError_t launch_softmax_t(const float *scores, uint16_t *probs, uint32_t S, uint32_t bh, float scale,
+                            uint32_t causal, hipStream_t stream) {
     uint32_t T = 0;
     const int nv = softmax_geometry(S, &T);
     const dim3 grid((uint32_t)((uint64_t)S * bh)), block(T);
     switch (nv) {
-    case 1: hipLaunchKernelGGL(nc_materialized_softmax<1>, grid, block, 0, stream, scores, probs, S, scale, causal); break;
-    case 2: hipLaunchKernelGGL(nc_materialized_softmax<2>, grid, block, 0, stream, scores, probs, S, scale, causal); break;
-    case 4: hipLaunchKernelGGL(nc_materialized_softmax<4>, grid, block, 0, stream, scores, probs, S, scale, causal); break;
-    case 8: hipLaunchKernelGGL(nc_materialized_softmax<8>, grid, block, 0, stream, scores, probs, S, scale, causal); break;
-    case 16: hipLaunchKernelGGL(nc_materialized_softmax<16>, grid, block, 0, stream, scores, probs, S, scale, causal); break;
-    case 32: hipLaunchKernelGGL(nc_materialized_softmax<32>, grid, block, 0, stream, scores, probs, S, scale, causal); break;
+    case 1: hipLaunchKernelGGL((nc_materialized_softmax<1, BF>), grid, block, 0, stream, scores, probs, S, scale, causal); break;
+    case 2: hipLaunchKernelGGL((nc_materialized_softmax<2, BF>), grid, block, 0, stream, scores, probs, S, scale, causal); break;
+    case 4: hipLaunchKernelGGL((nc_materialized_softmax<4, BF>), grid, block, 0, stream, scores, probs, S, scale, causal); break;
+    case 8: hipLaunchKernelGGL((nc_materialized_softmax<8, BF>), grid, block, 0, stream, scores, probs, S, scale, causal); break;
+    case 16: hipLaunchKernelGGL((nc_materialized_softmax<16, BF>), grid, block, 0, stream, scores, probs, S, scale, causal); break;
+    case 32: hipLaunchKernelGGL((nc_materialized_softmax<32, BF>), grid, block, 0, stream, scores, probs, S, scale, causal); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_softmax(const float *scores, uint16_t *probs, uint32_t S, uint32_t bh, float scale, uint32_t causal,
+                          bool bf16, hipStream_t stream) {
+    return bf16 ? launch_softmax_t<true>(scores, probs, S, bh, scale, causal, stream)
+                : launch_softmax_t<false>(scores, probs, S, bh, scale, causal, stream);
 }
 
 bool fits_i32(uint64_t x) { return x <= (uint64_t)std::numeric_limits<int32_t>::max(); }
@@ -215,7 +239,9 @@ int nc_materialized_attention(nc_materialized plan, const uint16_t *q, size_t q_
         return fail(NC_ERROR_INVALID_VALUE, me, "dimension beyond 32 bits");
 
     float *scores = static_cast<float *>(workspace);
-    _Float16 *probs = reinterpret_cast<_Float16 *>(static_cast<char *>(workspace) + S * S * bh * sizeof(float));
+    uint16_t *probs = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + S * S * bh * sizeof(float));
+    const bool bf16 = op.element_type == NC_ELEMENT_BF16;
+    const rocblas_datatype et = bf16 ? rocblas_datatype_bf16_r : rocblas_datatype_f16_r;
     const rocblas_int n = (rocblas_int)S, kd = (rocblas_int)d, batch = (rocblas_int)bh;
     const rocblas_stride ss = (rocblas_stride)(S * S);
     const float one = 1.f, zero = 0.f;
@@ -227,13 +253,14 @@ int nc_materialized_attention(nc_materialized plan, const uint16_t *q, size_t q_
     if (st) return st;
     st = check_rocblas(
         rocblas_gemm_strided_batched_ex(plan->handle, rocblas_operation_transpose, rocblas_operation_none, n, n, kd,
-                                        &one, k, rocblas_datatype_f16_r, (rocblas_int)kr, (rocblas_stride)op.k_stride,
-                                        q, rocblas_datatype_f16_r, (rocblas_int)qr, (rocblas_stride)op.q_stride, &zero,
+                                        &one, k, et, (rocblas_int)kr, (rocblas_stride)op.k_stride,
+                                        q, et, (rocblas_int)qr, (rocblas_stride)op.q_stride, &zero,
                                         scores, rocblas_datatype_f32_r, n, ss, scores, rocblas_datatype_f32_r, n, ss,
                                         batch, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
         "rocblas_gemm_strided_batched_ex (Q K^T)");
     if (st) return st;
-    st = check_hip(launch_softmax(scores, probs, (uint32_t)S, (uint32_t)bh, op.scale, op.causal ? 1u : 0u, plan->stream),
+    st = check_hip(launch_softmax(scores, probs, (uint32_t)S, (uint32_t)bh, op.scale, op.causal ? 1u : 0u, bf16,
+                                  plan->stream),
                    "nc_materialized_softmax launch");
     if (st) return st;
     // V as a d x S column-major matrix is V^T, probs as an S x S one is P^T: C = V^T P^T = (P V)^T,
@@ -241,8 +268,8 @@ int nc_materialized_attention(nc_materialized plan, const uint16_t *q, size_t q_
     // leading elements of each O row are written.
     return check_rocblas(
         rocblas_gemm_strided_batched_ex(plan->handle, rocblas_operation_none, rocblas_operation_none, kd, n, n, &one, v,
-                                        rocblas_datatype_f16_r, (rocblas_int)vr, (rocblas_stride)op.v_stride, probs,
-                                        rocblas_datatype_f16_r, n, ss, &zero, o, rocblas_datatype_f32_r,
+                                        et, (rocblas_int)vr, (rocblas_stride)op.v_stride, probs,
+                                        et, n, ss, &zero, o, rocblas_datatype_f32_r,
                                         (rocblas_int)orow, (rocblas_stride)op.o_stride, o, rocblas_datatype_f32_r,
                                         (rocblas_int)orow, (rocblas_stride)op.o_stride, batch, rocblas_datatype_f32_r,
                                         rocblas_gemm_algo_standard, 0, 0),

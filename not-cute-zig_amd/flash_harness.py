@@ -65,13 +65,20 @@ def modular_fill(n: int, mul: int, add: int, mod: int, scale: float) -> np.ndarr
     return ((((i * mul + add) % mod).astype(np.float32)) * np.float32(scale)).astype(np.float16).view(np.uint16)
 
 
+def decode(bits: np.ndarray, dtype: str = "f16") -> np.ndarray:
+    """16-bit patterns of f16 or bf16 (the upper half of a binary32) as float64."""
+    if dtype == "bf16":
+        return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    return bits.view(np.float16).astype(np.float64)
+
+
 def attention_f64(wl: Workload, q: np.ndarray, k: np.ndarray, v: np.ndarray,
                   rows: Optional[np.ndarray] = None) -> np.ndarray:
     """softmax(scale * Q K^T, causal mask) V in float64 for every slice; returns O in the workload's
     f32 layout with unwritten (pad) positions left 0. `rows` restricts the query rows computed."""
     S, D = wl.seq_len, wl.head_dim
     out = np.zeros(wl.length("o"), dtype=np.float64)
-    qf, kf, vf = (x.view(np.float16).astype(np.float64) for x in (q, k, v))
+    qf, kf, vf = (decode(x, wl.dtype) for x in (q, k, v))
     r_all = np.arange(S) if rows is None else np.asarray(rows)
     for b in range(wl.batch_heads):
         def mat(buf, which):

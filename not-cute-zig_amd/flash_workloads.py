@@ -42,6 +42,7 @@ class Workload:
     o_row: int = 0
     note: str = ""
     tags: List[str] = field(default_factory=list)
+    dtype: str = "f16"  # element type of Q/K/V: "f16" (the reference's) or "bf16"
 
     def row(self, which: str) -> int:
         r = getattr(self, f"{which}_row")
@@ -59,19 +60,23 @@ class Workload:
                           q_stride=self.stride("q"), k_stride=self.stride("k"), v_stride=self.stride("v"),
                           o_stride=self.stride("o"), scale=self.scale, causal=self.causal,
                           q_row_stride=self.q_row, k_row_stride=self.k_row, v_row_stride=self.v_row,
-                          o_row_stride=self.o_row)
+                          o_row_stride=self.o_row, dtype=self.dtype)
 
     def make_inputs(self) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """Q, K, V as 16-bit patterns of the workload's element type (the same seeded draws for
+        f16 and bf16, each rounded to nearest even)."""
+        bf = self.dtype == "bf16"
         out = []
         for tid, which in enumerate("qkv"):
             n = self.length(which)
             d = self.dists[tid]
             if d[0] == "normal":
-                out.append(nc.fill_normal(n, self.seed, tid, d[1], d[2]))
+                out.append((nc.fill_normal_bf16 if bf else nc.fill_normal)(n, self.seed, tid, d[1], d[2]))
             elif d[0] == "uniform":
-                out.append(nc.fill_uniform(n, self.seed, tid, d[1], d[2]))
+                out.append((nc.fill_uniform_bf16 if bf else nc.fill_uniform)(n, self.seed, tid, d[1], d[2]))
             elif d[0] == "pattern":
-                out.append(nc.fill_flash_input(n, d[1], d[2], d[3]))
+                h = nc.fill_flash_input(n, d[1], d[2], d[3])
+                out.append(_f16_to_bf16_exact(h) if bf else h)
             else:
                 raise ValueError(d)
         return tuple(out)
@@ -83,6 +88,14 @@ class Workload:
     def describe(self) -> str:
         return (f"{self.name}: BH={self.batch_heads} S={self.seq_len} d={self.head_dim} "
                 f"causal={self.causal} scale={self.scale:g}")
+
+
+def _f16_to_bf16_exact(h: np.ndarray) -> np.ndarray:
+    """f16 patterns whose values bf16 holds exactly (the reference's small dyadic fills)."""
+    bits = h.view(np.float16).astype(np.float32).view(np.uint32)
+    if np.any(bits & 0xFFFF):
+        raise ValueError("value not representable in bf16")
+    return (bits >> 16).astype(np.uint16)
 
 
 def _normal(s=1.0):

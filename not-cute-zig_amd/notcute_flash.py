@@ -40,6 +40,10 @@ class NcError(RuntimeError):
         super().__init__(msg)
 
 
+# element_type values (NC_ELEMENT_F16 / NC_ELEMENT_BF16).
+ELEMENT_TYPES = {"f16": 0, "bf16": 1}
+
+
 class FlashOptions(ctypes.Structure):
     """flash.Options (src/flash.zig:5-14) + optional row strides (0 = head_dim)."""
 
@@ -57,6 +61,7 @@ class FlashOptions(ctypes.Structure):
         ("k_row_stride", ctypes.c_uint64),
         ("v_row_stride", ctypes.c_uint64),
         ("o_row_stride", ctypes.c_uint64),
+        ("element_type", ctypes.c_uint32),
     ]
 
 
@@ -243,6 +248,10 @@ _SIGS = {
     "nc_fill_normal_f16": (None, [_P, ctypes.c_size_t, _U64, ctypes.c_uint32, ctypes.c_float, ctypes.c_float]),
     "nc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
     "nc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "nc_fill_uniform_bf16": (None, [_P, ctypes.c_size_t, _U64, ctypes.c_uint32, ctypes.c_float, ctypes.c_float]),
+    "nc_fill_normal_bf16": (None, [_P, ctypes.c_size_t, _U64, ctypes.c_uint32, ctypes.c_float, ctypes.c_float]),
+    "nc_f32_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),
+    "nc_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -282,9 +291,10 @@ def check(status: int, what: str) -> None:
 def options(*, seq_len: int, head_dim: int, q_stride: Optional[int] = None, k_stride: Optional[int] = None,
             v_stride: Optional[int] = None, o_stride: Optional[int] = None, scale: Optional[float] = None,
             batch_heads: int = 1, causal: bool = False, q_row_stride: int = 0, k_row_stride: int = 0,
-            v_row_stride: int = 0, o_row_stride: int = 0) -> FlashOptions:
+            v_row_stride: int = 0, o_row_stride: int = 0, dtype: str = "f16") -> FlashOptions:
     """Build flash.Options; unspecified slice strides default to the dense seq_len*head_dim and an
-    unspecified scale to 1/sqrt(head_dim) (the reference's callers, src/main.zig:225, 983)."""
+    unspecified scale to 1/sqrt(head_dim) (the reference's callers, src/main.zig:225, 983).
+    dtype "f16" (the reference's) or "bf16" sets element_type."""
     o = FlashOptions()
     lib().nc_flash_options_init(ctypes.byref(o))
     dense = seq_len * head_dim
@@ -301,6 +311,7 @@ def options(*, seq_len: int, head_dim: int, q_stride: Optional[int] = None, k_st
     o.k_row_stride = k_row_stride
     o.v_row_stride = v_row_stride
     o.o_row_stride = o_row_stride
+    o.element_type = ELEMENT_TYPES[dtype]
     return o
 
 
@@ -596,6 +607,28 @@ def fill_normal(n: int, seed: int, tensor_id: int, mean: float = 0.0, sigma: flo
     out = np.empty(n, dtype=np.uint16)
     lib().nc_fill_normal_f16(out.ctypes.data, n, seed, tensor_id, mean, sigma)
     return out
+
+
+def fill_uniform_bf16(n: int, seed: int, tensor_id: int, lo: float = -1.0, hi: float = 1.0) -> np.ndarray:
+    """The draws of fill_uniform rounded to bf16 bit patterns."""
+    out = np.empty(n, dtype=np.uint16)
+    lib().nc_fill_uniform_bf16(out.ctypes.data, n, seed, tensor_id, lo, hi)
+    return out
+
+
+def fill_normal_bf16(n: int, seed: int, tensor_id: int, mean: float = 0.0, sigma: float = 1.0) -> np.ndarray:
+    """The draws of fill_normal rounded to bf16 bit patterns."""
+    out = np.empty(n, dtype=np.uint16)
+    lib().nc_fill_normal_bf16(out.ctypes.data, n, seed, tensor_id, mean, sigma)
+    return out
+
+
+def f32_to_bf16(x: float) -> int:
+    return int(lib().nc_f32_to_bf16(x))
+
+
+def bf16_to_f32(h: int) -> float:
+    return float(lib().nc_bf16_to_f32(h))
 
 
 def f32_to_f16(x: float) -> int:

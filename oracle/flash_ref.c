@@ -14,6 +14,8 @@
  *     o[row][c] = sum_key (weight[key] / row_sum) * f32(v[key][c]), keys in order  (:1298-1305)
  * Generalised with a row stride per tensor (0 = head_dim, the reference layout). Only the active
  * rows x head_dim region of each O slice is written; padding keeps whatever the caller put there.
+ * oracle_flash_fwd_typed also takes bf16 inputs (an extension: the reference's inputs are f16);
+ * they are widened exactly to f32 and the same loop nest runs.
  *
  * Two rearrangements keep every result bit-identical to the loop nest above while making it fast
  * enough for the large configurations: (1) weight[key] / row_sum is computed once per key instead of
@@ -58,6 +60,16 @@ static float half_to_float(uint16_t h) {
 }
 
 float oracle_half_to_float(uint16_t h) { return half_to_float(h); }
+
+/* bfloat16 is the upper half of a binary32: widening is exact. */
+static float bf16_to_float(uint16_t h) {
+    const uint32_t x = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+float oracle_bf16_to_float(uint16_t h) { return bf16_to_float(h); }
 
 typedef struct {
     int64_t S, D;
@@ -149,12 +161,13 @@ static void *row_worker(void *arg) {
  * must be < seq_len). threads <= 1 runs on the calling thread. Returns 0, or -1 on bad arguments or
  * allocation failure.
  */
-int oracle_flash_fwd(uint64_t batch_heads, uint64_t seq_len, uint64_t head_dim, const uint16_t *q,
-                     uint64_t q_stride, uint64_t q_row, const uint16_t *k, uint64_t k_stride, uint64_t k_row,
-                     const uint16_t *v, uint64_t v_stride, uint64_t v_row, float *o, uint64_t o_stride,
-                     uint64_t o_row, float scale, uint32_t causal, int threads, const int64_t *rows,
-                     uint64_t nrows) {
-    if (!q || !k || !v || !o || seq_len == 0 || head_dim == 0) return -1;
+int oracle_flash_fwd_typed(uint64_t batch_heads, uint64_t seq_len, uint64_t head_dim, const uint16_t *q,
+                           uint64_t q_stride, uint64_t q_row, const uint16_t *k, uint64_t k_stride, uint64_t k_row,
+                           const uint16_t *v, uint64_t v_stride, uint64_t v_row, float *o, uint64_t o_stride,
+                           uint64_t o_row, float scale, uint32_t causal, int threads, const int64_t *rows,
+                           uint64_t nrows, uint32_t element_type) {
+    if (!q || !k || !v || !o || seq_len == 0 || head_dim == 0 || element_type > 1) return -1;
+    float (*widen)(uint16_t) = element_type == 1 ? bf16_to_float : half_to_float;
     const int64_t S = (int64_t)seq_len, D = (int64_t)head_dim;
     if (!q_row) q_row = head_dim;
     if (!k_row) k_row = head_dim;
@@ -177,9 +190,9 @@ int oracle_flash_fwd(uint64_t batch_heads, uint64_t seq_len, uint64_t head_dim, 
         const uint16_t *qs = q + b * q_stride, *ks = k + b * k_stride, *vs = v + b * v_stride;
         for (int64_t r = 0; r < S; ++r)
             for (int64_t c = 0; c < D; ++c) {
-                qf[r * D + c] = half_to_float(qs[r * (int64_t)q_row + c]);
-                kt[c * S + r] = half_to_float(ks[r * (int64_t)k_row + c]);
-                vf[r * D + c] = half_to_float(vs[r * (int64_t)v_row + c]);
+                qf[r * D + c] = widen(qs[r * (int64_t)q_row + c]);
+                kt[c * S + r] = widen(ks[r * (int64_t)k_row + c]);
+                vf[r * D + c] = widen(vs[r * (int64_t)v_row + c]);
             }
         slice_ctx ctx = {S, D, qf, kt, vf, o + b * o_stride, (int64_t)o_row, scale, causal != 0};
         row_pool pool;
@@ -212,4 +225,14 @@ int oracle_flash_fwd(uint64_t batch_heads, uint64_t seq_len, uint64_t head_dim, 
     free(kt);
     free(vf);
     return rc;
+}
+
+/* f16 inputs: the reference's oracle. */
+int oracle_flash_fwd(uint64_t batch_heads, uint64_t seq_len, uint64_t head_dim, const uint16_t *q,
+                     uint64_t q_stride, uint64_t q_row, const uint16_t *k, uint64_t k_stride, uint64_t k_row,
+                     const uint16_t *v, uint64_t v_stride, uint64_t v_row, float *o, uint64_t o_stride,
+                     uint64_t o_row, float scale, uint32_t causal, int threads, const int64_t *rows,
+                     uint64_t nrows) {
+    return oracle_flash_fwd_typed(batch_heads, seq_len, head_dim, q, q_stride, q_row, k, k_stride, k_row, v, v_stride,
+                                  v_row, o, o_stride, o_row, scale, causal, threads, rows, nrows, 0);
 }

@@ -23,6 +23,14 @@ from flash_workloads import Workload
 MAX_ABS = 2e-3
 MAX_REL = 1e-2
 REL_FLOOR = 0.2
+# bf16 extension: weights rounded to bf16 (8 significant bits) for the PV product.
+BF16_MAX_ABS = 8e-3
+BF16_MAX_REL = 4e-2
+
+
+def parity_bar(dtype: str = "f16") -> Tuple[float, float]:
+    """(max-abs, max-rel) bar of the element type."""
+    return (BF16_MAX_ABS, BF16_MAX_REL) if dtype == "bf16" else (MAX_ABS, MAX_REL)
 SENTINEL = np.float32(-7777.0)
 
 
@@ -47,7 +55,7 @@ def oracle(wl: Workload, q, k, v, rows=None, o_init: Optional[np.ndarray] = None
                            q_stride=wl.stride("q"), k_stride=wl.stride("k"), v_stride=wl.stride("v"),
                            o_stride=wl.stride("o"), scale=wl.scale, causal=wl.causal, q_row=wl.row("q"),
                            k_row=wl.row("k"), v_row=wl.row("v"), o_row=wl.row("o"),
-                           threads=host_threads() if threads is None else threads, rows=rows)
+                           threads=host_threads() if threads is None else threads, rows=rows, dtype=wl.dtype)
     return o
 
 
