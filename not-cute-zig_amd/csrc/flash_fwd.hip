@@ -882,20 +882,70 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         });
     }
 
-    // Epilogue. (1) Each wave publishes its per-query (m, l) in a dedicated LDS area (no wave
-    // reads the staging ring any more once it is past its loop, but others may still be in theirs,
-    // so the ring is not touched yet). (2) After one barrier every lane derives, for its query, the
-    // merge weight exp2(m_s - M) / L of its own partial (M = max over the NS key splits,
-    // L = sum exp2(m_j - M) l_j), scales its O^T partial in registers and writes it over the ring.
-    // (3) After a second barrier each output float4 is the plain sum of NS scaled partials, stored
-    // row-contiguously (coalesced).
+    constexpr int DC = D / 4;
     float2v *mlb = reinterpret_cast<float2v *>(smem + C::ML_OFF);  // [BM queries][NS splits]
     const float lt = pair_sum(l);
+    if constexpr (PRIV && NS > 1) {
+        // Epilogue, private staging: once a wave is past its loop, the K and V slices of ring
+        // stage 0 that only it ever loaded are free, so it writes its unscaled O^T partial there
+        // (queries 0-15 over its K slice, 16-31 over its V slice, 16-byte chunks XOR-swizzled by
+        // row) and its (m, l) in the dedicated area, all before the single barrier. Then each output
+        // float4 is sum_j w_j o_j / L with w_j = exp2(m_j - M), M = max_j m_j, L = sum_j w_j l_j
+        // over the NS key splits (w_j = 0 for a split that saw no key), stored row-contiguously.
+        constexpr int SLICE = 64 * D;  // bytes of one wave's 32 staged rows of K (or V)
+        auto part = [&](int split, int q, int chunk) {
+            const int lr = q & 15;
+            return reinterpret_cast<floatx4 *>(smem + (q < 16 ? 0 : C::TILE) + split * SLICE + lr * 4 * D +
+                                               ((chunk ^ (lr & (DC - 1))) << 4));
+        };
+        if (hh == 0) mlb[c * NS + s] = float2v{mrow, lt};
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 32 * mt + 8 * i + 4 * hh;
+                if (d < D) *part(s, c, d >> 2) = floatx4{o[mt][4 * i], o[mt][4 * i + 1], o[mt][4 * i + 2], o[mt][4 * i + 3]};
+            }
+        wait_vm_barrier<0>();
+        for (int u = tid; u < C::BM * DC; u += C::NT) {
+            const int qi = u / DC, ch = u % DC;
+            const int row = q0 + qi;
+            if (row >= S) continue;
+            float2v ml[NS];
+            floatx4 pj[NS];
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                ml[j] = mlb[qi * NS + j];
+                pj[j] = *part(j, qi, ch);
+            }
+            float mmax = ml[0][0];
+#pragma unroll
+            for (int j = 1; j < NS; ++j) mmax = fmaxf(mmax, ml[j][0]);
+            float den = 0.f;
+            floatx4 res = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                const float wj = __builtin_amdgcn_exp2f(ml[j][0] - mmax);  // exp2(-inf) = 0
+                den = __builtin_fmaf(wj, ml[j][1], den);
+                res += wj * pj[j];
+            }
+            __builtin_nontemporal_store(res * __builtin_amdgcn_rcpf(den),
+                                        reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch));
+        }
+        return;
+    }
+
+    // Epilogue, shared staging. (1) Each wave publishes its per-query (m, l) in a dedicated LDS
+    // area (other waves may still read the ring). (2) After one barrier every lane derives, for
+    // its query, the merge weight exp2(m_s - M) / L of its own partial (M = max over the NS key
+    // splits, L = sum exp2(m_j - M) l_j), scales its O^T partial in registers and writes it over
+    // the ring. (3) After a second barrier each output float4 is the plain sum of NS scaled
+    // partials, stored row-contiguously (coalesced). With NS = 1 the weight is 1 / l.
     if (hh == 0) mlb[(qg * 32 + c) * NS + s] = float2v{mrow, lt};
     wait_vm_barrier<0>();
     float scale_own;
     if constexpr (NS == 1) {
-        scale_own = 1.f / lt;
+        scale_own = __builtin_amdgcn_rcpf(lt);
     } else {
         const float2v *row = mlb + (qg * 32 + c) * NS;
         float2v ml[NS];
@@ -906,8 +956,8 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         for (int j = 1; j < NS; ++j) mmax = fmaxf(mmax, ml[j][0]);
         float den = 0.f;
 #pragma unroll
-        for (int j = 0; j < NS; ++j) den += __builtin_amdgcn_exp2f(ml[j][0] - mmax) * ml[j][1];
-        scale_own = __builtin_amdgcn_exp2f(mrow - mmax) / den;  // exp2(-inf) = 0 for empty splits
+        for (int j = 0; j < NS; ++j) den = __builtin_fmaf(__builtin_amdgcn_exp2f(ml[j][0] - mmax), ml[j][1], den);
+        scale_own = __builtin_amdgcn_exp2f(mrow - mmax) * __builtin_amdgcn_rcpf(den);  // 0 for empty splits
     }
     float *ob = reinterpret_cast<float *>(smem);
     {
@@ -924,15 +974,17 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             }
     }
     __syncthreads();
-    constexpr int DC = D / 4;
     for (int u = tid; u < C::BM * DC; u += C::NT) {
         const int qi = u / DC, ch = u % DC;
         const int row = q0 + qi;
         if (row >= S) continue;
         const float *src = ob + ((qi / 32) * NS * 32 + (qi % 32)) * C::OP + 4 * ch;
-        floatx4 res = *reinterpret_cast<const floatx4 *>(src);
+        floatx4 parts[NS];
 #pragma unroll
-        for (int j = 1; j < NS; ++j) res += *reinterpret_cast<const floatx4 *>(src + 32 * j * C::OP);
+        for (int j = 0; j < NS; ++j) parts[j] = *reinterpret_cast<const floatx4 *>(src + 32 * j * C::OP);
+        floatx4 res = parts[0];
+#pragma unroll
+        for (int j = 1; j < NS; ++j) res += parts[j];
         __builtin_nontemporal_store(res, reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch));
     }
 }
