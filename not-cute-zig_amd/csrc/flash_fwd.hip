@@ -5,27 +5,32 @@
 // src/flash_h64_bn32.zig:26, src/flash_h64_causal.zig:20, src/kernels.zig:380). Same math:
 // O = softmax(scale * Q K^T, causal mask) V per (batch, head) slice, f16 inputs, f32 accumulation,
 // f32 output, online softmax over key tiles with the row max/sum rescale of
-// src/flash_h64_bn32.zig:139-211, P rounded to f16 for the PV product while the row sum uses the
-// unrounded weights (src/flash_h64_bn32.zig:180-185), final O / l (src/flash_h64_bn32.zig:246-260).
+// src/flash_h64_bn32.zig:139-211 and the final O / l of src/flash_h64_bn32.zig:246-260. P is rounded
+// to f16 for the PV product; the generic kernels sum the unrounded weights as the reference does
+// (src/flash_h64_bn32.zig:180-185), the pipelined kernels sum the rounded ones, so that numerator
+// and denominator use the same P.
 //
-// gfx950 formulation
+// gfx950 formulation, common to both kernel families
 //   * One wave owns 32 queries. It computes the transposed score tile S^T = K * Q^T with
 //     v_mfma_f32_32x32x16_f16 (A = K rows from LDS, B = Q^T held in VGPRs for the whole sweep).
 //     In the 32x32 accumulator layout lane l holds column (query) l%32 and 16 rows (keys)
 //     8*(r/4) + 4*(l/32) + r%4, so the softmax row statistics of a query live in one lane pair
-//     (l, l^32): max and sum are 15 in-lane ops plus one v_permlane32_swap.
+//     (l, l^32): max and sum are in-lane ops plus one v_permlane32_swap.
 //   * The exponentiated tile P^T is already in the B-operand layout of the PV product
 //     O^T += V^T * P^T (registers 0..7 -> keys 0..15, 8..15 -> keys 16..31), so P never touches LDS.
-//     V^T is staged transposed in LDS with keys permuted to match (bits 2 and 3 of the key index
-//     within each 16-key group swapped), which turns every A-operand fetch into one ds_read_b128.
 //   * A workgroup has NQ x NS waves: NQ query groups of 32 rows, each of whose key range is split
-//     over NS waves (key sub-tile j of every BN = 32*NS staged keys goes to wave j). NS > 1 fills
-//     the chip on short sequences; the NS partial (m, l, O) triples are merged through LDS with the
-//     same rescale rule. All variants share the LDS epilogue, which also coalesces the f32 stores.
+//     over NS waves. NS > 1 fills the chip on short sequences; the NS partial (m, l, O) triples are
+//     merged through LDS with the same rescale rule, and the LDS epilogue also coalesces the f32
+//     stores.
 //   * Causal: key sub-tiles entirely above the diagonal are skipped per wave, and key blocks past
 //     the workgroup's last query are never staged. Heavy (late) query blocks are dispatched first and
 //     workgroups of the same heads are kept on one XCD so their K/V stay in that XCD's L2.
 //   * exp is v_exp_f32 on log2-scaled scores (scale * log2(e) folded into one multiply).
+// The generic family (flash_fwd_body: any 16-byte aligned layout, 64-bit addressing, and element-wise
+// variants for unaligned ones) stages K/V through registers and stores V^T transposed in LDS with
+// keys permuted so each A-operand fetch is one ds_read_b128. The pipelined family
+// (flash_fwd_pipe_body, the fast path) streams K/V with buffer->LDS DMA into a ring and reads V^T
+// with ds_read_b64_tr_b16; it is described where it is defined.
 //   * Every kernel also exists with a `_bf16` suffix: bf16 Q/K/V, probabilities rounded to bf16 for
 //     the PV product, v_mfma_f32_32x32x16_bf16 (an extension; the reference computes in f16 only).
 
@@ -417,11 +422,14 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
 // per row against bank conflicts; the Q K^T A-operand is one ds_read_b128 per 16 head columns, and
 // the V^T A-operand of the PV product is assembled by ds_read_b64_tr_b16: inside each 16-lane group
 // lane m points at V[r0 + m/4][d0 + 4(m%4)], and lane i receives V[r0..r0+3][d0 + i].
-// One s_barrier per block (no fence): each wave first waits on its own loads of that block.
+// Shared staging (several query groups): one s_barrier per block (no fence), each wave first
+// waiting on its own loads of that block. Private staging (one query group, NQ = 1): each wave
+// loads and reads only its own key slice, so the loop has no barrier at all.
+// The softmax keeps a lazy running max: weights are formed against the max as it stands and the
+// max only moves when a weight overflows (or, before the first tile, when a row has none).
 // ---------------------------------------------------------------------------------------------
 
 #define NC_LDS(T) __attribute__((address_space(3))) T
-typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
 // LDS layout of a staged K or V block: row r (a key), 16-byte chunk ch (8 head columns) stored at
 // slot r*CH + (ch ^ f(r)). f is chosen for the two read patterns on gfx950's 64 x 4-byte banks:
