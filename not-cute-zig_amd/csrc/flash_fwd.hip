@@ -754,9 +754,6 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         // S^T for SUB consecutive 32-key sub-tiles (independent MFMA chains).
         floatx16 acc[SUB];
         half8 kf[SUB * (D / 16)];
-        // MFMA groups run at raised wave priority, so the matrix cores take work from whichever
-        // wave has it while the others are in their softmax.
-        __builtin_amdgcn_s_setprio(1);
         static_for<0, SUB>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             acc[j] = floatx16{};
@@ -767,7 +764,6 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             }
         });
         lds_reads_done(kf);
-        __builtin_amdgcn_s_setprio(0);
         // V^T operands, issued once every K read of this step has landed (lds_reads_done orders
         // them) so their latency hides behind the softmax. ds_read_b64_tr_b16 goes through asm:
         // the builtin is treated as aliasing the in-flight buffer->LDS loads of later blocks, and
@@ -842,6 +838,10 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             mrow = m_new;
             neg_m = (mrow == neg_inf()) ? 0.f : -mrow;
         };
+        // Non-causal shared staging: the softmax runs at raised wave priority (measured 1.5 % faster on
+        // long sequences; causal and private-staging variants are fastest at the default priority).
+        constexpr bool SOFTMAX_PRIO = !PRIV && !CAUSAL;
+        if constexpr (SOFTMAX_PRIO) __builtin_amdgcn_s_setprio(1);
         float ls;
         if (__builtin_amdgcn_ballot_w64(mrow == neg_inf())) {
             to_tile_max();  // some row has no max yet: take it first
@@ -854,9 +854,9 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             }
         }
         l += ls;
+        if constexpr (SOFTMAX_PRIO) __builtin_amdgcn_s_setprio(0);
 
         wait_lds_tied(vt);
-        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int j = 0; j < SUB; ++j)
 #pragma unroll
@@ -867,7 +867,6 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                     const u32x4 vv = {v4[0][0], v4[0][1], v4[1][0], v4[1][1]};
                     o[mt] = mfma32<BF>(__builtin_bit_cast(half8, vv), pf[j][ks], o[mt]);
                 }
-        __builtin_amdgcn_s_setprio(0);
     };
 
     // Prologue: blocks 0 .. NSTAGE-2 in flight; then Q (issued before them) has landed once at most
