@@ -131,11 +131,14 @@ const Variant *choose_pipe(const nc_flash_options &o) {
         return find_pipe(d, 1, 8, causal, bf);
     }
     if (d == 32) {
-        if ((S <= 512 && wgs(128) >= 512) || (S <= 1024 && wgs(128) >= 1024)) return find_pipe(d, 4, 1, causal, bf);
-        if (wgs(64) >= (causal ? 1024u : 512u)) return find_pipe(d, 2, 4, causal, bf);
+        if ((S <= (causal ? 256u : 512u) && wgs(128) >= 512) || (S <= 1024 && wgs(128) >= 1024))
+            return find_pipe(d, 4, 1, causal, bf);
+        if (causal ? (wgs(64) >= 1024 && (S <= 4096 || wgs(64) >= 2048)) : wgs(64) >= 512)
+            return find_pipe(d, 2, 4, causal, bf);
         return find_pipe(d, 1, 8, causal, bf);
     }
-    if (wgs(64) >= 1024) return find_pipe(d, 2, 4, causal, bf);
+    // d = 16: long sequences over few heads keep the 8 key splits unless the grid is large.
+    if (wgs(64) >= 1024 && (S <= 2048 || wgs(64) >= 2048)) return find_pipe(d, 2, 4, causal, bf);
     return find_pipe(d, 1, 8, causal, bf);
 }
 
