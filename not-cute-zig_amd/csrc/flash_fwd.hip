@@ -663,7 +663,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     }
 
     // One query group per workgroup: every wave consumes only its own key slice of each block,
-    // so each wave stages that slice itself and no barrier is needed until the epilogue; a wave
+    // so each wave stages that slice itself and the key loop needs no barrier; a wave
     // runs only over the blocks where its slice has visible keys.
     constexpr bool PRIV = (NQ == 1);
     const int kv_end = CAUSAL ? min(S, q0 + C::BM) : S;
