@@ -43,8 +43,8 @@ struct Variant {
         const uint32_t o_bytes = nw * 32 * (d + 4) * 4;
         if (family == Family::kPipe) {
             const uint32_t ring = nstage * 2 * bn() * d * 2;
-            // + (m, l) area, + the Q tile of a one-query-group workgroup
-            return (ring > o_bytes ? ring : o_bytes) + nw * 32 * 2 * 4 + (nq == 1 ? 32 * d * 2 : 0);
+            // + (m, l) area, + the workgroup's Q tile when key-split waves share it
+            return (ring > o_bytes ? ring : o_bytes) + nw * 32 * 2 * 4 + (ns > 1 ? bm() * d * 2 : 0);
         }
         const uint32_t dv = d < 32 ? 32 : d;
         const uint32_t stage = bn() * (d + 8) * 2 + dv * (bn() + 8) * 2;

@@ -592,8 +592,11 @@ struct PipeCfg {
     static constexpr int OP = D + 4;
     static constexpr int O_BYTES = NW * 32 * OP * 4;
     static constexpr int ML_OFF = RING > O_BYTES ? RING : O_BYTES;
-    static constexpr int Q_OFF = ML_OFF + NW * 32 * 2 * 4;                // Q tile (private staging)
-    static constexpr int LDS_BYTES = Q_OFF + (NQ == 1 ? 32 * D * 2 : 0);
+    static constexpr bool QLDS = NS > 1;                                   // Q staged once in LDS
+    static constexpr int QLOADS = BM * CH / 64;                            // its wave-instructions
+    static_assert(!QLDS || QLOADS <= NW, "one Q load per wave at most");
+    static constexpr int Q_OFF = ML_OFF + NW * 32 * 2 * 4;
+    static constexpr int LDS_BYTES = Q_OFF + (QLDS ? BM * D * 2 : 0);
     static constexpr int MT = D < 32 ? 1 : D / 32;
 };
 
@@ -644,13 +647,13 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     float *obase = a.o + (size_t)head * a.o_stride;
     const size_t ors = a.o_row_stride;
 
-    // Q^T B-operand (rows past seq_len read as zero), waited for after the prologue. With one
-    // query group per workgroup every wave needs the same 32 rows: the first CH/2 waves copy them
-    // once into an LDS tile (1 KB each, same swizzle as K), read by all after one barrier, instead
-    // of each wave fetching the whole tile from L2.
+    // Q^T B-operand (rows past seq_len read as zero), waited for after the prologue. With NS key-split
+    // waves per query group, NS waves need the same 32 rows: the workgroup's BM rows are copied once
+    // into an LDS tile (1 KB per wave-instruction, same swizzle as K) and read by every wave after
+    // one barrier, instead of each wave fetching its group's rows from L2.
     half8 qf[D / 16];
-    if constexpr (NQ == 1) {
-        if (w < C::CH / 2) {
+    if constexpr (C::QLDS) {
+        if (w < C::QLOADS) {
             const __amdgpu_buffer_rsrc_t qrr = make_rsrc(a.q + (size_t)head * a.q_stride, qspan);
             const int p = w * 64 + lane;
             const int r = p / C::CH, sl = p % C::CH;
@@ -890,11 +893,11 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         if (I < nblk) issue(I, IC<I>{});
     });
     with_clamped<0, (NSTAGE > 1 ? NSTAGE - 1 : 1)>(nblk, [&](auto ac) { wait_vm_only<decltype(ac)::value * C::LPW>(); });
-    if constexpr (NQ == 1) {
+    if constexpr (C::QLDS) {
         asm volatile("s_barrier" ::: "memory");  // every wave's part of the Q tile has landed
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk)
-            qf[kk] = *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(lds0 + C::Q_OFF + SW::slot(c, 2 * kk + hh) * 16));
+            qf[kk] = *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(lds0 + C::Q_OFF + SW::slot(32 * qg + c, 2 * kk + hh) * 16));
     }
     tie_regs(qf);
     if (neg_q) {
