@@ -54,12 +54,15 @@ struct Variant {
 
 #define PIPE(D, NQ, NS, P, C, T, BF) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "_" C T, D, NQ, NS, P, 1, \
                                       C[0] == 'c', true, Family::kPipe, BF}
+// Two 32-key sub-tiles per wave per block ("t2": 32*NS*2 keys per block).
+#define PIPE2(D, NQ, NS, P, C, T, BF) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "t2_" C T, D, NQ, NS, P, 2, \
+                                       C[0] == 'c', true, Family::kPipe, BF}
 #define GEN(D, C, A, SUF, T, BF) {"nc_flash_fwd_d" #D "_m64_" C SUF T, D, 2, 2, 1, 1, C[0] == 'c', A, \
                                   Family::kGeneric, BF}
 // Every kernel of the family, once per element type (T: name suffix, BF: bf16).
 #define VARIANTS(T, BF)                                                                                         \
-    PIPE(64, 8, 1, 3, "full", T, BF), PIPE(64, 8, 1, 3, "causal", T, BF), PIPE(64, 4, 1, 3, "full", T, BF),     \
-    PIPE(64, 4, 1, 3, "causal", T, BF), PIPE(64, 2, 4, 2, "full", T, BF), PIPE(64, 2, 4, 2, "causal", T, BF),   \
+    PIPE2(64, 8, 1, 2, "full", T, BF), PIPE2(64, 8, 1, 2, "causal", T, BF), PIPE2(64, 4, 1, 2, "full", T, BF),  \
+    PIPE2(64, 4, 1, 2, "causal", T, BF), PIPE(64, 2, 4, 2, "full", T, BF), PIPE(64, 2, 4, 2, "causal", T, BF),  \
     PIPE(64, 1, 8, 2, "full", T, BF), PIPE(64, 1, 8, 2, "causal", T, BF), PIPE(32, 4, 1, 3, "full", T, BF),     \
     PIPE(32, 4, 1, 3, "causal", T, BF), PIPE(32, 2, 4, 2, "full", T, BF), PIPE(32, 2, 4, 2, "causal", T, BF),   \
     PIPE(32, 1, 8, 2, "full", T, BF), PIPE(32, 1, 8, 2, "causal", T, BF), PIPE(16, 2, 4, 2, "full", T, BF),     \
@@ -73,12 +76,12 @@ struct Variant {
 const Variant kVariants[] = {VARIANTS("", false), VARIANTS("_bf16", true)};
 #undef VARIANTS
 #undef PIPE
+#undef PIPE2
 #undef GEN
 
 const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal, bool bf16) {
     for (const auto &v : kVariants)
-        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.sub == 1 && v.causal == causal &&
-            v.bf16 == bf16)
+        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.causal == causal && v.bf16 == bf16)
             return &v;
     return nullptr;
 }
@@ -109,15 +112,16 @@ const char *reference_kernel(const nc_flash_options &o) {
 }
 
 // MI355X dispatch (256 CUs). Wider query blocks share every staged K/V tile among more waves, so
-// they are preferred while the grid still gives every CU at least one workgroup; short or few
-// sequences move to narrower query blocks whose keys are split over more waves, so that even the
-// heaviest (causal: last) query block finishes in a few key-block steps.
-// Chosen from GPU sweeps of every variant over BH x S x d x causal (48 + 42 shapes). The shared-
-// staging kernels (q8s1, q4s1, q2s4) need enough workgroups to fill the CUs twice over; causal
-// masking makes their per-workgroup work uneven, so they need more of them (or short sequences)
-// before they beat the private-staging q1s8, whose 8 key-split waves stay balanced on any grid.
-// The bf16 twins have the same instruction stream (bf16 MFMA, conversion and dot forms instead of
-// the f16 ones) and follow the same rule.
+// they are preferred once the grid gives every CU enough workgroups; short or few sequences move to
+// narrower query blocks whose keys are split over more waves, so that even the heaviest (causal:
+// last) query block finishes in a few key-block steps.
+// Chosen from GPU sweeps of every variant over BH x S x d x causal (102 shapes for d=64, 56 for
+// d=16/32, interleaved timing). At d=64 the 128-VGPR q2s4 runs two workgroups per CU and wins the
+// middle ground: causal masking makes the shared-staging kernels' per-workgroup work uneven, so
+// causal shapes need more workgroups (or short sequences) before q8s1 or q2s4 beat the private-
+// staging q1s8, whose 8 key-split waves stay balanced on any grid. The bf16 twins have the same
+// instruction stream (bf16 MFMA, conversion and dot forms instead of the f16 ones) and follow the
+// same rule.
 const Variant *choose_pipe(const nc_flash_options &o) {
     const uint32_t d = (uint32_t)o.head_dim;
     const bool causal = o.causal != 0;
@@ -125,21 +129,28 @@ const Variant *choose_pipe(const nc_flash_options &o) {
     const uint64_t S = o.seq_len;
     auto wgs = [&](uint64_t bm) { return ((S + bm - 1) / bm) * o.batch_heads; };
     if (d == 64) {
-        if (causal && S <= 512 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal, bf);
-        if (causal ? (wgs(256) >= 512 || (wgs(256) >= 256 && S <= 1024)) : wgs(256) >= 256)
-            return find_pipe(d, 8, 1, causal, bf);
-        if (wgs(64) >= 256 && (!causal || o.batch_heads >= 2)) return find_pipe(d, 2, 4, causal, bf);
+        if (causal) {
+            if (wgs(256) >= 512 && (S <= 4096 || wgs(256) >= 1024)) return find_pipe(d, 8, 1, causal, bf);
+            if (S <= 512 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal, bf);
+            if (wgs(64) >= (S <= 1024 ? 256u : 512u)) return find_pipe(d, 2, 4, causal, bf);
+            return find_pipe(d, 1, 8, causal, bf);
+        }
+        if (S <= 256 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal, bf);
+        if (wgs(256) >= 256) return find_pipe(d, 8, 1, causal, bf);
+        if (wgs(64) >= 256) return find_pipe(d, 2, 4, causal, bf);
         return find_pipe(d, 1, 8, causal, bf);
     }
     if (d == 32) {
         if ((S <= (causal ? 256u : 512u) && wgs(128) >= 512) || (S <= 1024 && wgs(128) >= 1024))
             return find_pipe(d, 4, 1, causal, bf);
-        if (causal ? (wgs(64) >= 1024 && (S <= 4096 || wgs(64) >= 2048)) : wgs(64) >= 512)
+        if ((causal ? (wgs(64) >= 1024 && (S <= 4096 || wgs(64) >= 2048)) : wgs(64) >= 512) ||
+            (S <= 256 && wgs(64) >= 256))
             return find_pipe(d, 2, 4, causal, bf);
         return find_pipe(d, 1, 8, causal, bf);
     }
     // d = 16: long sequences over few heads keep the 8 key splits unless the grid is large.
-    if (wgs(64) >= 1024 && (S <= 2048 || wgs(64) >= 2048)) return find_pipe(d, 2, 4, causal, bf);
+    if ((wgs(64) >= 1024 && (S <= 4096 || wgs(64) >= 2048)) || (S <= 256 && wgs(64) >= 256))
+        return find_pipe(d, 2, 4, causal, bf);
     return find_pipe(d, 1, 8, causal, bf);
 }
 

@@ -738,66 +738,34 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt) o[mt] = floatx16{};
 
-    // One key block: wait for its stage, refill the stage consumed last step, compute this wave's
-    // 32x32 sub-tile.
-    auto step = [&](int blk, auto stage_c) {
-        constexpr int ST = decltype(stage_c)::value;
-        if constexpr (PRIV && NSTAGE == 1) {
-            // Private single stage: the wave's reads of the previous block are complete (their
-            // results were consumed), so it refills the stage with this block and waits for it.
-            if (blk > 0) issue(blk, IC<0>{});
-            wait_vm_only<0>();
-        } else if constexpr (PRIV) {
-            wait_vm_own<C::LPW, NSTAGE - 2>(min(NSTAGE - 2, nblk - 1 - blk));
-            if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
-        } else if constexpr (NSTAGE == 1) {
-            // Single stage: refill it once every wave is done with the previous block.
-            if (blk > 0) {
-                __builtin_amdgcn_s_waitcnt(0xc07f & ~(0xf << 8));  // lgkmcnt(0)
-                asm volatile("s_barrier" ::: "memory");
-                issue(blk, IC<0>{});
-            }
-            wait_vm_barrier<0>();
-        } else {
-            wait_block<C::LPW, NSTAGE - 2>(min(NSTAGE - 2, nblk - 1 - blk));
-            if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
-        }
+    // One 32x32 sub-tile of this wave: S^T = K Q^T for its 32 keys (kt0 ..), online softmax, and
+    // O^T += V^T P^T. TOFF is the sub-tile's byte offset in the LDS ring (a compile-time constant).
+    auto tile = [&](const int kt0, auto toff_c) {
+        constexpr int TOFF = decltype(toff_c)::value;
 
-        const int kt0 = blk * C::BN + C::WK * s;  // this wave's first key
-        bool run = kt0 < S;
-        if (CAUSAL) run = run && kt0 <= qw_last;
-        if (!run) return;
-
-        // S^T for SUB consecutive 32-key sub-tiles (independent MFMA chains).
-        floatx16 acc[SUB];
-        half8 kf[SUB * (D / 16)];
-        static_for<0, SUB>([&](auto jc) {
-            constexpr int j = decltype(jc)::value;
-            acc[j] = floatx16{};
+        // S^T of the sub-tile.
+        floatx16 acc = floatx16{};
+        half8 kf[D / 16];
 #pragma unroll
-            for (int kk = 0; kk < D / 16; ++kk) {
-                kf[j * (D / 16) + kk] = lds_load_b128<ST * C::STAGE + 2 * j * ROW16>(kaddr[kk]);
-                acc[j] = mfma32<BF>(kf[j * (D / 16) + kk], qf[kk], acc[j]);
-            }
-        });
+        for (int kk = 0; kk < D / 16; ++kk) {
+            kf[kk] = lds_load_b128<TOFF>(kaddr[kk]);
+            acc = mfma32<BF>(kf[kk], qf[kk], acc);
+        }
         lds_reads_done(kf);
         // V^T operands, issued once every K read of this step has landed (lds_reads_done orders
         // them) so their latency hides behind the softmax. ds_read_b64_tr_b16 goes through asm:
         // the builtin is treated as aliasing the in-flight buffer->LDS loads of later blocks, and
         // the compiler would drain them (vmcnt(0)) before every read. wait_lds_tied() waits for
         // these reads and ties the registers to that wait.
-        u32x2 vt[SUB * C::MT * 4];
-        static_for<0, SUB>([&](auto jc) {
-            constexpr int j = decltype(jc)::value;
+        u32x2 vt[C::MT * 4];
 #pragma unroll
-            for (int mt = 0; mt < C::MT; ++mt) {
-                u32x2 *v4 = vt + (j * C::MT + mt) * 4;
-                ds_read_tr<ST * C::STAGE + 2 * j * ROW16>(v4[0], vaddr[mt][0]);
-                ds_read_tr<ST * C::STAGE + 2 * j * ROW16>(v4[1], vaddr[mt][1]);
-                ds_read_tr<ST * C::STAGE + 2 * j * ROW16 + ROW16>(v4[2], vaddr[mt][0]);
-                ds_read_tr<ST * C::STAGE + 2 * j * ROW16 + ROW16>(v4[3], vaddr[mt][1]);
-            }
-        });
+        for (int mt = 0; mt < C::MT; ++mt) {
+            u32x2 *v4 = vt + mt * 4;
+            ds_read_tr<TOFF>(v4[0], vaddr[mt][0]);
+            ds_read_tr<TOFF>(v4[1], vaddr[mt][1]);
+            ds_read_tr<TOFF + ROW16>(v4[2], vaddr[mt][0]);
+            ds_read_tr<TOFF + ROW16>(v4[3], vaddr[mt][1]);
+        }
 
         // Online softmax (sc > 0). P = exp2(sc * s - m) is formed against the running max m as it
         // stands and rounded to f16 for the PV product; the row sum adds the rounded weights
@@ -807,46 +775,51 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         // the tile max is taken - before scaling, exact since rounding is monotonic - O and l
         // are rescaled and the tile is redone. Once a row has a max its sum is >= 1, so small
         // weights cannot underflow it.
-        const bool need_mask = (kt0 + C::WK > S) || (CAUSAL && kt0 + C::WK - 1 > qw0);
+        const bool need_mask = (kt0 + 32 > S) || (CAUSAL && kt0 + 31 > qw0);
         if (need_mask) {
-            const int lim = CAUSAL ? min(qrow, S - 1) - kt0 : S - 1 - kt0;  // last visible key offset
-#pragma unroll
-            for (int j = 0; j < SUB; ++j)
+            // lim: the last visible key offset in the sub-tile. The shared-staging kernels fold this
+            // lane's 4*hh into it, so every element compares against an inline constant and no
+            // per-element key offsets stay live across their register-tight key loop; the
+            // private-staging kernels have registers to spare and keep the offsets precomputed.
+            if constexpr (PRIV) {
+                const int lim = CAUSAL ? min(qrow, S - 1) - kt0 : S - 1 - kt0;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    if (32 * j + 8 * (r >> 2) + 4 * hh + (r & 3) > lim) acc[j][r] = neg_inf();
+                    if (8 * (r >> 2) + 4 * hh + (r & 3) > lim) acc[r] = neg_inf();
+            } else {
+                const int lim = (CAUSAL ? min(qrow, S - 1) - kt0 : S - 1 - kt0) - 4 * hh;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (8 * (r >> 2) + (r & 3) > lim) acc[r] = neg_inf();
+            }
         }
-        half8 pf[SUB][2];
+        half8 pf[2];
         auto weights = [&]() {
             float ls = 0.f;
 #pragma unroll
-            for (int j = 0; j < SUB; ++j)
+            for (int ks = 0; ks < 2; ++ks) {
+                half2v h[4];
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    half2v h[4];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        h[t] = round2<BF>(__builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][8 * ks + 2 * t], sc, neg_m)),
-                                          __builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][8 * ks + 2 * t + 1], sc, neg_m)));
-                        pf[j][ks][2 * t] = h[t][0];
-                        pf[j][ks][2 * t + 1] = h[t][1];
-                    }
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) ls = sum2<BF>(h[t], ls);
+                for (int t = 0; t < 4; ++t) {
+                    h[t] = round2<BF>(__builtin_amdgcn_exp2f(__builtin_fmaf(acc[8 * ks + 2 * t], sc, neg_m)),
+                                      __builtin_amdgcn_exp2f(__builtin_fmaf(acc[8 * ks + 2 * t + 1], sc, neg_m)));
+                    pf[ks][2 * t] = h[t][0];
+                    pf[ks][2 * t + 1] = h[t][1];
                 }
+#pragma unroll
+                for (int t = 0; t < 4; ++t) ls = sum2<BF>(h[t], ls);
+            }
             return ls;
         };
         // Move the running max to the tile max (rows whose max does not grow keep it) and rescale.
         auto to_tile_max = [&]() {
-            float tmax = neg_inf();
-#pragma unroll
-            for (int j = 0; j < SUB; ++j) {
-                const floatx16 &x = acc[j];
-                const float m0 = fmaxf(fmaxf(x[0], x[1]), x[2]), m1 = fmaxf(fmaxf(x[3], x[4]), x[5]);
-                const float m2 = fmaxf(fmaxf(x[6], x[7]), x[8]), m3 = fmaxf(fmaxf(x[9], x[10]), x[11]);
-                const float m4 = fmaxf(fmaxf(x[12], x[13]), x[14]);
-                tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), x[15])));
-            }
+            const floatx16 &x = acc;
+            const float m0 = fmaxf(fmaxf(x[0], x[1]), x[2]), m1 = fmaxf(fmaxf(x[3], x[4]), x[5]);
+            const float m2 = fmaxf(fmaxf(x[6], x[7]), x[8]), m3 = fmaxf(fmaxf(x[9], x[10]), x[11]);
+            const float m4 = fmaxf(fmaxf(x[12], x[13]), x[14]);
+            // (folding -inf in first lets the compiler fuse the tree into v_max3 without extra
+            // canonicalising maxes)
+            const float tmax = fmaxf(neg_inf(), fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), x[15])));
             const float m_new = fmaxf(mrow, pair_max(tmax) * sc);
             const float alpha = __builtin_amdgcn_exp2f(mrow - (m_new == neg_inf() ? 0.f : m_new));
             l *= alpha;
@@ -875,15 +848,51 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
 
         wait_lds_tied(vt);
 #pragma unroll
-        for (int j = 0; j < SUB; ++j)
+        for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
-            for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const u32x2 *v4 = vt + (j * C::MT + mt) * 4 + 2 * ks;
-                    const u32x4 vv = {v4[0][0], v4[0][1], v4[1][0], v4[1][1]};
-                    o[mt] = mfma32<BF>(__builtin_bit_cast(half8, vv), pf[j][ks], o[mt]);
-                }
+            for (int ks = 0; ks < 2; ++ks) {
+                const u32x2 *v4 = vt + mt * 4 + 2 * ks;
+                const u32x4 vv = {v4[0][0], v4[0][1], v4[1][0], v4[1][1]};
+                o[mt] = mfma32<BF>(__builtin_bit_cast(half8, vv), pf[ks], o[mt]);
+            }
+    };
+    // One key block: wait for its stage, refill the stage consumed last step, compute this wave's
+    // sub-tiles.
+    auto step = [&](int blk, auto stage_c) {
+        constexpr int ST = decltype(stage_c)::value;
+        if constexpr (PRIV && NSTAGE == 1) {
+            // Private single stage: the wave's reads of the previous block are complete (their
+            // results were consumed), so it refills the stage with this block and waits for it.
+            if (blk > 0) issue(blk, IC<0>{});
+            wait_vm_only<0>();
+        } else if constexpr (PRIV) {
+            wait_vm_own<C::LPW, NSTAGE - 2>(min(NSTAGE - 2, nblk - 1 - blk));
+            if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
+        } else if constexpr (NSTAGE == 1) {
+            // Single stage: refill it once every wave is done with the previous block.
+            if (blk > 0) {
+                __builtin_amdgcn_s_waitcnt(0xc07f & ~(0xf << 8));  // lgkmcnt(0)
+                asm volatile("s_barrier" ::: "memory");
+                issue(blk, IC<0>{});
+            }
+            wait_vm_barrier<0>();
+        } else {
+            wait_block<C::LPW, NSTAGE - 2>(min(NSTAGE - 2, nblk - 1 - blk));
+            if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
+        }
+
+        // The wave's keys in the block are SUB consecutive 32-key sub-tiles, each taken through S^T,
+        // softmax and PV before the next (one sub-tile's operands live at a time), so a block of
+        // 32*NS*SUB keys costs one wait and one barrier.
+        const int kb = blk * C::BN + C::WK * s;  // the wave's first key in the block
+        bool run = kb < S;
+        if (CAUSAL) run = run && kb <= qw_last;
+        if (!run) return;
+        static_for<0, SUB>([&](auto jc) {
+            constexpr int TOFF = ST * C::STAGE + 2 * decltype(jc)::value * ROW16;  // sub-tile in the stage
+            tile(kb + 32 * decltype(jc)::value, IC<TOFF>{});
+            __builtin_amdgcn_sched_barrier(0);  // keep sub-tiles (and steps) apart
+        });
     };
 
     // Prologue: blocks 0 .. NSTAGE-2 in flight; then Q (issued before them) has landed once at most
@@ -989,9 +998,11 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         for (int j = 0; j < NS; ++j) den = __builtin_fmaf(__builtin_amdgcn_exp2f(ml[j][0] - mmax), ml[j][1], den);
         scale_own = __builtin_amdgcn_exp2f(mrow - mmax) * __builtin_amdgcn_rcpf(den);  // 0 for empty splits
     }
-    float *ob = reinterpret_cast<float *>(smem);
+    // 32-bit LDS pointers: with generic ones the compiler keeps 64-bit address parts live across
+    // the key loop of these register-tight kernels.
+    NC_LDS(float) *ob = reinterpret_cast<NC_LDS(float) *>((uintptr_t)lds0);
     {
-        float *dst = ob + (w * 32 + c) * C::OP;
+        NC_LDS(float) *dst = ob + (w * 32 + c) * C::OP;
 #pragma unroll
         for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
@@ -999,7 +1010,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 const int d = 32 * mt + 8 * i + 4 * hh;
                 if (d < D) {
                     floatx4 t = {o[mt][4 * i], o[mt][4 * i + 1], o[mt][4 * i + 2], o[mt][4 * i + 3]};
-                    *reinterpret_cast<floatx4 *>(dst + d) = t * scale_own;
+                    *reinterpret_cast<NC_LDS(floatx4) *>(dst + d) = t * scale_own;
                 }
             }
     }
@@ -1008,10 +1019,10 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         const int qi = u / DC, ch = u % DC;
         const int row = q0 + qi;
         if (row >= S) continue;
-        const float *src = ob + ((qi / 32) * NS * 32 + (qi % 32)) * C::OP + 4 * ch;
+        const NC_LDS(float) *src = ob + ((qi / 32) * NS * 32 + (qi % 32)) * C::OP + 4 * ch;
         floatx4 parts[NS];
 #pragma unroll
-        for (int j = 0; j < NS; ++j) parts[j] = *reinterpret_cast<const floatx4 *>(src + 32 * j * C::OP);
+        for (int j = 0; j < NS; ++j) parts[j] = *reinterpret_cast<const NC_LDS(floatx4) *>(src + 32 * j * C::OP);
         floatx4 res = parts[0];
 #pragma unroll
         for (int j = 1; j < NS; ++j) res += parts[j];
@@ -1223,10 +1234,10 @@ extern "C" __global__ __launch_bounds__(256) void nc_util_copy_b128(const u32x4 
     }
 
 // Pipelined variants: q = query waves (32 rows each), s = key-split waves, p = LDS ring depth.
-NC_FLASH_PIPE_KERNEL_WPE(nc_flash_fwd_d64_q8s1p3_full, 64, 8, 1, false, 3, 1, 4)
-NC_FLASH_PIPE_KERNEL_WPE(nc_flash_fwd_d64_q8s1p3_causal, 64, 8, 1, true, 3, 1, 4)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_full, 64, 4, 1, false, 3, 1)
-NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p3_causal, 64, 4, 1, true, 3, 1)
+NC_FLASH_PIPE_KERNEL_WPE(nc_flash_fwd_d64_q8s1p2t2_full, 64, 8, 1, false, 2, 2, 4)
+NC_FLASH_PIPE_KERNEL_WPE(nc_flash_fwd_d64_q8s1p2t2_causal, 64, 8, 1, true, 2, 2, 4)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p2t2_full, 64, 4, 1, false, 2, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q4s1p2t2_causal, 64, 4, 1, true, 2, 2)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_full, 64, 2, 4, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_causal, 64, 2, 4, true, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_full, 64, 1, 8, false, 2, 1)

@@ -167,7 +167,8 @@ def test_dispatch_geometry(d, causal, bh, s):
     assert f"_d{d}_" in name and name.endswith("_causal" if causal else "_full")
     assert sel.threads % 64 == 0 and 64 <= sel.threads <= 1024
     assert sel.grid[0] == -(-s // sel.block_m) * bh and sel.grid[1] == sel.grid[2] == 1
-    assert sel.block_m % 32 == 0 and sel.block_n == 32 * sel.kv_splits
+    # 32 or 64 keys per key-split wave per staged block (one or two 32-key sub-tiles)
+    assert sel.block_m % 32 == 0 and sel.block_n in (32 * sel.kv_splits, 64 * sel.kv_splits)
     assert sel.threads == 2 * sel.block_m * sel.kv_splits  # (block_m/32) query waves x splits x 64 lanes
     assert 0 < sel.lds_bytes <= 160 * 1024
     assert sel.aligned == 1
@@ -175,8 +176,8 @@ def test_dispatch_geometry(d, causal, bh, s):
 
 def test_dispatch_headline_and_large_configs():
     assert nc.select_kernel(CONFIGS["c3"].options()).name == b"nc_flash_fwd_d64_q1s8p2_causal"
-    assert nc.select_kernel(CONFIGS["c4"].options()).name == b"nc_flash_fwd_d64_q8s1p3_full"
-    assert nc.select_kernel(CONFIGS["c5"].options()).name == b"nc_flash_fwd_d64_q8s1p3_causal"
+    assert nc.select_kernel(CONFIGS["c4"].options()).name == b"nc_flash_fwd_d64_q8s1p2t2_full"
+    assert nc.select_kernel(CONFIGS["c5"].options()).name == b"nc_flash_fwd_d64_q8s1p2t2_causal"
 
 
 def test_dispatch_alignment_fallbacks():
