@@ -926,6 +926,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         // row) and its (m, l) in the dedicated area, all before the single barrier. Then each output
         // float4 is sum_j w_j o_j / L with w_j = exp2(m_j - M), M = max_j m_j, L = sum_j w_j l_j
         // over the NS key splits (w_j = 0 for a split that saw no key), stored row-contiguously.
+        static_assert(SUB == 1, "a wave's staged slice is 32 rows");
         constexpr int SLICE = 64 * D;  // bytes of one wave's 32 staged rows of K (or V)
         auto part = [&](int split, int q, int chunk) {
             const int lr = q & 15;
