@@ -425,6 +425,9 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
 // Shared staging (several query groups): one s_barrier per block (no fence), each wave first
 // waiting on its own loads of that block. Private staging (one query group, NQ = 1): each wave
 // loads and reads only its own key slice, so the loop has no barrier at all.
+// A wave's keys in a block are SUB consecutive 32-key sub-tiles, each taken through S^T, softmax
+// and PV before the next. Kernels with key-split waves (NS > 1) stage the workgroup's Q rows in LDS
+// once instead of every wave loading its group's rows.
 // The softmax keeps a lazy running max: weights are formed against the max as it stands and the
 // max only moves when a weight overflows (or, before the first tile, when a row has none).
 // ---------------------------------------------------------------------------------------------
