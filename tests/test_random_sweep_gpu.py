@@ -14,7 +14,7 @@ from flash_workloads import Workload, sample_rows
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 48
+N_CASES = 160
 
 
 def random_case(i: int):
