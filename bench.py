@@ -39,8 +39,9 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(wl, q, k, v, budget_s: float) -> dict:
-    """Time the CPU oracle (single thread) on the full workload, repeated until `budget_s` passes."""
+def cpu_baseline(wl, q, k, v, budget_s: float, threads: int = 1) -> dict:
+    """Time the CPU oracle (`threads` host threads over (slice, row)) on the full workload, repeated
+    until `budget_s` passes."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import flash_oracle  # noqa: E402  (checker / CPU baseline only)
 
@@ -50,7 +51,7 @@ def cpu_baseline(wl, q, k, v, budget_s: float) -> dict:
     while True:
         flash_oracle.flash_fwd(q, k, v, o, batch_heads=wl.batch_heads, seq_len=wl.seq_len, head_dim=wl.head_dim,
                                q_stride=wl.stride("q"), k_stride=wl.stride("k"), v_stride=wl.stride("v"),
-                               o_stride=wl.stride("o"), scale=wl.scale, causal=wl.causal, threads=1,
+                               o_stride=wl.stride("o"), scale=wl.scale, causal=wl.causal, threads=threads,
                                dtype=wl.dtype)
         reps += 1
         el = time.perf_counter() - t0
@@ -60,9 +61,10 @@ def cpu_baseline(wl, q, k, v, budget_s: float) -> dict:
     return {
         "value": flops * reps / el / 1e12,
         "unit": "TFLOP/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"full {wl.name} workload ({wl.describe()}) x {reps} repetitions, {el:.1f} s, one thread, "
+        "sample": f"full {wl.name} workload ({wl.describe()}) x {reps} repetitions, {el:.1f} s, "
+                  f"{'one thread' if threads == 1 else f'{threads} threads over (slice, row)'}, "
                   f"C restatement of src/main.zig:1271-1307 (-O3, no fast-math)",
     }, o
 
@@ -192,6 +194,21 @@ def main() -> int:
     log(f"bench: {steps} steps in {total_ms:.3f} ms -> {ms * 1e3:.3f} us/step; per-launch event timing "
         f"mean {per_launch.mean_ms * 1e3:.2f} us min {per_launch.min_ms * 1e3:.2f} us")
 
+    # Fixed per-launch cost: an empty kernel with the same grid and block, replayed the same way.
+    empty = mod.get_function("nc_util_empty")
+    egraph = nc.Graph.capture(stream, lambda: [empty.launch(tuple(sel.grid), (sel.threads,), [ka],
+                                                            stream=stream.handle) for _ in range(gb)])
+    egraph.launch(stream)
+    stream.synchronize()
+    ev0.record(stream.handle)
+    for _ in range(reps):
+        egraph.launch(stream)
+    ev1.record(stream.handle)
+    ev1.synchronize()
+    floor_ms = nc.Event.elapsed(ev0, ev1) / steps
+    egraph.destroy()
+    log(f"bench: empty kernel with the same grid: {floor_ms * 1e3:.3f} us/launch")
+
     if args.calibrate_copy:
         calibrate_copy(mod, stream, args.calibrate_copy << 20, 10)
 
@@ -215,10 +232,15 @@ def main() -> int:
         roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(tflops / PEAK_F16_TFLOPS, 5), "traffic": traffic}
 
-    cpu = None
+    cpu = cpu_all = None
     if args.cpu_seconds > 0:
         cpu, _ = cpu_baseline(wl, q, k, v, args.cpu_seconds)
         log(f"bench: cpu baseline {cpu['value'] * 1e3:.3f} GFLOP/s ({cpu['sample']})")
+        # the same oracle threaded over (slice, row) on the host cores this job may use (16 on the box)
+        nthr = max(1, min(16, len(os.sched_getaffinity(0))))
+        if nthr > 1:
+            cpu_all, _ = cpu_baseline(wl, q, k, v, args.cpu_seconds / 2, threads=nthr)
+            log(f"bench: cpu baseline, {nthr} threads: {cpu_all['value'] * 1e3:.3f} GFLOP/s")
 
     rec = {
         "metric": "flash-attn fwd TFLOP/s + % f16 MFMA peak, BH=8 S=1024 d=64 causal",
@@ -247,9 +269,13 @@ def main() -> int:
         "timing": "HIP events around graph replays of back-to-back launches on the launch stream",
         "per_launch_event_ms": {"mean": per_launch.mean_ms, "min": per_launch.min_ms, "max": per_launch.max_ms,
                                 "iters": args.ref_iters},
+        "launch_floor": {"ms_per_step": round(floor_ms, 6), "kernel": "nc_util_empty",
+                         "grid": list(sel.grid), "threads": sel.threads,
+                         "timing": "same graph replays as the timed region, empty kernel body"},
         "parity_max_abs": max_abs,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baseline_threads": cpu_all,
     }
     print(json.dumps(rec), flush=True)
     for b in (dq, dk, dv, do):

@@ -166,6 +166,11 @@ int nc_graph_destroy(nc_graph graph);
  * nc_util_copy_b128(const uint4 *src, uint4 *dst, uint64_t n16), grid-stride loop over n16 items. */
 #define NC_UTIL_COPY_KERNEL "nc_util_copy_b128"
 
+/* Name of an empty kernel taking the flash kernels' argument block, launched by the benchmark with
+ * a flash kernel's grid and block to time the fixed dispatch-and-completion cost of one launch:
+ * nc_util_empty(nc_flash_kernel_args), does nothing. */
+#define NC_UTIL_EMPTY_KERNEL "nc_util_empty"
+
 /* ------------------------------------------------------------------------------------------------
  * Flash-attention forward (src/flash.zig:5-100).
  * ---------------------------------------------------------------------------------------------- */

@@ -124,10 +124,18 @@ __device__ __forceinline__ u32x4 load8(const uint16_t *p) {
     }
 }
 
+// One 16-byte O store, written through to memory at system scope (sc0 sc1) as a streaming (nt)
+// access. A kernel's completion writes back every dirty L2 line it left, on the critical path of
+// the launch; a written-through O leaves none. Measured on MI355X against a non-temporal
+// write-back store: BH=8 S=1024 d=64 causal 6.06 -> 5.87 us, long sequences unchanged (-0.1 %).
+__device__ __forceinline__ void store_o(floatx4 *p, floatx4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(p), "v"(v) : "memory");
+}
+
 template <bool VEC>
 __device__ __forceinline__ void store4(float *p, floatx4 v) {
     if constexpr (VEC) {
-        *reinterpret_cast<floatx4 *>(p) = v;
+        store_o(reinterpret_cast<floatx4 *>(p), v);
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = v[i];
@@ -967,8 +975,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 den = __builtin_fmaf(wj, ml[j][1], den);
                 res += wj * pj[j];
             }
-            __builtin_nontemporal_store(res * __builtin_amdgcn_rcpf(den),
-                                        reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch));
+            store_o(reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch), res * __builtin_amdgcn_rcpf(den));
         }
         return;
     }
@@ -1025,7 +1032,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         floatx4 res = parts[0];
 #pragma unroll
         for (int j = 1; j < NS; ++j) res += parts[j];
-        __builtin_nontemporal_store(res, reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch));
+        store_o(reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch), res);
     }
 }
 
@@ -1211,6 +1218,10 @@ NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_causal_unaligned, 64, 2, 2, true, false)
 extern "C" __global__ __launch_bounds__(256) void nc_util_copy_b128(const u32x4 *src, u32x4 *dst, uint64_t n16) {
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256ull) dst[i] = src[i];
 }
+
+// Empty kernel with the flash kernels' argument block: launched with a flash kernel's grid, it
+// times the fixed per-launch dispatch and completion cost that no kernel body can remove.
+extern "C" __global__ __launch_bounds__(1024) void nc_util_empty(nc_flash_kernel_args a) { (void)a; }
 
 // Each instantiation defines NAME (f16) and NAME_bf16.
 #define NC_FLASH_PIPE_KERNEL(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB)                              \
