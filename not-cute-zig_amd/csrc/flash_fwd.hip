@@ -6,9 +6,9 @@
 // O = softmax(scale * Q K^T, causal mask) V per (batch, head) slice, f16 inputs, f32 accumulation,
 // f32 output, online softmax over key tiles with the row max/sum rescale of
 // src/flash_h64_bn32.zig:139-211 and the final O / l of src/flash_h64_bn32.zig:246-260. P is rounded
-// to f16 for the PV product; the generic kernels sum the unrounded weights as the reference does
-// (src/flash_h64_bn32.zig:180-185), the pipelined kernels sum the rounded ones, so that numerator
-// and denominator use the same P.
+// to f16 for the PV product; the generic kernels and most pipelined ones sum the unrounded weights
+// as the reference does (src/flash_h64_bn32.zig:180-185), the q2s4 and d=32 q4s1 pipelined kernels
+// sum the rounded ones (numerator and denominator then use the same P).
 //
 // gfx950 formulation, common to both kernel families
 //   * One wave owns 32 queries. It computes the transposed score tile S^T = K * Q^T with
@@ -99,11 +99,14 @@ __device__ __forceinline__ float sum2(half2v p, float acc) {
     }
 }
 // A 32-key tile's weight sum (per lane, 16 weights) at or above this moves the running max to the
-// tile max. f16: only an overflowed (infinite) weight does. bf16 has f32's range, so weights are
-// held below 2^20 to keep the f32 row sum and O accumulators far from overflow.
-template <bool BF>
+// tile max. f16: a weight that overflows f16 does; with the sum of the rounded weights (F32SUM
+// false) only that sum turns infinite, with the sum of the f32 weights (F32SUM true) a sum of 65504
+// or more is taken as the sign (a weight that rounds to infinity is at least 65520). bf16 has f32's
+// range, so weights are held below 2^20 to keep the f32 row sum and O accumulators far from
+// overflow.
+template <bool BF, bool F32SUM>
 __device__ __forceinline__ float weight_sum_limit() {
-    return BF ? 1048576.0f : __builtin_inff();
+    return BF ? 1048576.0f : F32SUM ? 65504.0f : __builtin_inff();
 }
 
 // Position of key kk (block-relative) inside a staged V^T row: swap bits 2 and 3.
@@ -738,6 +741,16 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // Log2-domain scale. A negative scale is applied by negating the resident Q operand (exact),
     // a zero scale by a tiny positive one (every score then rounds to weight exp2(0) = 1, as with
     // a zero scale), so the softmax below can assume sc > 0.
+    // Row sum of a tile: the f32 weights added by v_add_f32 (F32SUM), or the f16/bf16-rounded
+    // weights added by v_dot2c against 1.0 pairs. v_dot2c does not execute while an MFMA of the
+    // same SIMD is in flight (measured: 8 v_dot2c per 32x32x16 MFMA take longer than both run one
+    // after the other, where FMA, exp and the f16 packing hide the MFMAs entirely), so the f32 adds
+    // run faster, but keep 8 more VGPRs live. Interleaved A/B on MI355X: 1-1.7 % faster for the
+    // private-staging (q1s8) and d=64 one-split (q8s1, q4s1) kernels; the q2s4 kernels lose
+    // occupancy instead (d=16: 6 -> 5 waves per SIMD, 8.7 % slower; d=64: capped at the 128 VGPRs
+    // that let two workgroups share a CU, they spill) and d=32 q4s1 gains nothing, so those keep
+    // v_dot2c.
+    constexpr bool F32SUM = NS == 8 || (D == 64 && NS == 1);
     float sc = a.scale * kLog2e;
     const bool neg_q = sc < 0.f;  // Q is negated once it has landed
     if (neg_q) sc = -sc;
@@ -779,10 +792,10 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
 
         // Online softmax (sc > 0). P = exp2(sc * s - m) is formed against the running max m as it
-        // stands and rounded to f16 for the PV product; the row sum adds the rounded weights
-        // (v_dot2c against 1.0 pairs), so numerator and denominator use the same P. f16 keeps
-        // its relative precision up to 65504, so m only has to move when some weight overflows
-        // f16, which makes that lane's tile sum infinite; then (and while a row has no max yet)
+        // stands and rounded to f16 for the PV product; the row sum adds the f32 weights or the
+        // rounded ones (F32SUM). f16 keeps its relative precision up to 65504, so m only has to
+        // move when some weight overflows f16, which shows in that lane's tile sum (see
+        // weight_sum_limit); then (and while a row has no max yet)
         // the tile max is taken - before scaling, exact since rounding is monotonic - O and l
         // are rescaled and the tile is redone. Once a row has a max its sum is >= 1, so small
         // weights cannot underflow it.
@@ -806,21 +819,39 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
         half8 pf[2];
         auto weights = [&]() {
-            float ls = 0.f;
+            if constexpr (F32SUM) {
+                float part[2];
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                half2v h[4];
+                for (int ks = 0; ks < 2; ++ks) {
+                    float e[8];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    h[t] = round2<BF>(__builtin_amdgcn_exp2f(__builtin_fmaf(acc[8 * ks + 2 * t], sc, neg_m)),
-                                      __builtin_amdgcn_exp2f(__builtin_fmaf(acc[8 * ks + 2 * t + 1], sc, neg_m)));
-                    pf[ks][2 * t] = h[t][0];
-                    pf[ks][2 * t + 1] = h[t][1];
+                    for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[8 * ks + i], sc, neg_m));
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const half2v h = round2<BF>(e[2 * t], e[2 * t + 1]);
+                        pf[ks][2 * t] = h[0];
+                        pf[ks][2 * t + 1] = h[1];
+                    }
+                    part[ks] = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
                 }
+                return part[0] + part[1];
+            } else {
+                float ls = 0.f;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) ls = sum2<BF>(h[t], ls);
+                for (int ks = 0; ks < 2; ++ks) {
+                    half2v h[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        h[t] = round2<BF>(__builtin_amdgcn_exp2f(__builtin_fmaf(acc[8 * ks + 2 * t], sc, neg_m)),
+                                          __builtin_amdgcn_exp2f(__builtin_fmaf(acc[8 * ks + 2 * t + 1], sc, neg_m)));
+                        pf[ks][2 * t] = h[t][0];
+                        pf[ks][2 * t + 1] = h[t][1];
+                    }
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) ls = sum2<BF>(h[t], ls);
+                }
+                return ls;
             }
-            return ls;
         };
         // Move the running max to the tile max (rows whose max does not grow keep it) and rescale.
         auto to_tile_max = [&]() {
@@ -845,7 +876,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             ls = weights();
         } else {
             ls = weights();
-            if (__builtin_amdgcn_ballot_w64(!(ls < weight_sum_limit<BF>()))) {
+            if (__builtin_amdgcn_ballot_w64(!(ls < weight_sum_limit<BF, F32SUM>()))) {
                 to_tile_max();  // a weight overflowed (f16) or grew too large (bf16): redo the tile
                 ls = weights();
             }
