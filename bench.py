@@ -39,6 +39,18 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo ("unknown" where it is not readable)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(wl, q, k, v, budget_s: float, threads: int = 1) -> dict:
     """Time the CPU oracle (`threads` host threads over (slice, row)) on the full workload, repeated
     until `budget_s` passes."""
@@ -65,7 +77,7 @@ def cpu_baseline(wl, q, k, v, budget_s: float, threads: int = 1) -> dict:
         "kind": "port",
         "sample": f"full {wl.name} workload ({wl.describe()}) x {reps} repetitions, {el:.1f} s, "
                   f"{'one thread' if threads == 1 else f'{threads} threads over (slice, row)'}, "
-                  f"C restatement of src/main.zig:1271-1307 (-O3, no fast-math)",
+                  f"C restatement of src/main.zig:1271-1307 (-O3, no fast-math), on {cpu_model()}",
     }, o
 
 
@@ -182,9 +194,12 @@ def main() -> int:
     graph = nc.Graph.capture(stream, lambda: [launch() for _ in range(gb)])
     # warmup, part 2: the remaining warmup steps as replays of the timed graph, so the timed region
     # starts at the clock the GPU holds under this load (a GPU that has idled runs its first
-    # milliseconds of work on a lower clock)
-    for _ in range(max(1, (args.warmup - eager_warmup) // gb)):
+    # milliseconds of work on a lower clock). At most 10 graphs are in flight between synchronizes:
+    # under rocprofv3's kernel tracer, ~200 queued graphs of 100 launches crashed the host runtime.
+    for i in range(max(1, (args.warmup - eager_warmup) // gb)):
         graph.launch(stream)
+        if i % 10 == 9:
+            stream.synchronize()
     stream.synchronize()
     ev0, ev1 = nc.Event(), nc.Event()
     nc.synchronize()
