@@ -6,9 +6,9 @@
 // O = softmax(scale * Q K^T, causal mask) V per (batch, head) slice, f16 inputs, f32 accumulation,
 // f32 output, online softmax over key tiles with the row max/sum rescale of
 // src/flash_h64_bn32.zig:139-211 and the final O / l of src/flash_h64_bn32.zig:246-260. P is rounded
-// to f16 for the PV product; the generic kernels and most pipelined ones sum the unrounded weights
-// as the reference does (src/flash_h64_bn32.zig:180-185), the q2s4 and d=32 q4s1 pipelined kernels
-// sum the rounded ones (numerator and denominator then use the same P).
+// to f16 for the PV product; the generic kernels and most f16 pipelined ones sum the unrounded
+// weights as the reference does (src/flash_h64_bn32.zig:180-185), the q2s4, d=32 q4s1 and all bf16
+// pipelined kernels sum the rounded ones (numerator and denominator then use the same P).
 //
 // gfx950 formulation, common to both kernel families
 //   * One wave owns 32 queries. It computes the transposed score tile S^T = K * Q^T with
@@ -749,8 +749,11 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // private-staging (q1s8) and d=64 one-split (q8s1, q4s1) kernels; the q2s4 kernels lose
     // occupancy instead (d=16: 6 -> 5 waves per SIMD, 8.7 % slower; d=64: capped at the 128 VGPRs
     // that let two workgroups share a CU, they spill) and d=32 q4s1 gains nothing, so those keep
-    // v_dot2c.
-    constexpr bool F32SUM = NS == 8 || (D == 64 && NS == 1);
+    // v_dot2c. With unrounded weights in the denominator, the rounding of P biases O by up to
+    // the rounding's relative error times |V| when the dominant weights round the same way: 2^-12
+    // for f16, but 2^-9 for bf16, which breaks the bf16 bar on such inputs, so bf16 always sums the
+    // rounded weights (numerator and denominator then use the same P and the bias cancels).
+    constexpr bool F32SUM = !BF && (NS == 8 || (D == 64 && NS == 1));
     float sc = a.scale * kLog2e;
     const bool neg_q = sc < 0.f;  // Q is negated once it has landed
     if (neg_q) sc = -sc;
