@@ -215,6 +215,18 @@ def main() -> int:
     log(f"bench: {steps} steps in {total_ms:.3f} ms -> {ms * 1e3:.3f} us/step; per-launch event timing "
         f"mean {per_launch.mean_ms * 1e3:.2f} us min {per_launch.min_ms * 1e3:.2f} us")
 
+    # One event pair around 100 plain back-to-back launches (no graph), divided by 100.
+    for _ in range(10):
+        launch()
+    stream.synchronize()
+    ev0.record(stream.handle)
+    for _ in range(100):
+        launch()
+    ev1.record(stream.handle)
+    ev1.synchronize()
+    b2b_ms = nc.Event.elapsed(ev0, ev1) / 100
+    log(f"bench: 100 back-to-back launches without a graph: {b2b_ms * 1e3:.3f} us/launch")
+
     # Fixed per-launch cost: an empty kernel with the same grid and block, replayed the same way.
     empty = mod.get_function("nc_util_empty")
     egraph = nc.Graph.capture(stream, lambda: [empty.launch(tuple(sel.grid), (sel.threads,), [ka],
@@ -290,6 +302,7 @@ def main() -> int:
         "timing": "HIP events around graph replays of back-to-back launches on the launch stream",
         "per_launch_event_ms": {"mean": per_launch.mean_ms, "min": per_launch.min_ms, "max": per_launch.max_ms,
                                 "iters": args.ref_iters},
+        "back_to_back_launch_ms": round(b2b_ms, 6),
         "launch_floor": {"ms_per_step": round(floor_ms, 6), "kernel": "nc_util_empty",
                          "grid": list(sel.grid), "threads": sel.threads,
                          "timing": "same graph replays as the timed region, empty kernel body"},
