@@ -48,6 +48,13 @@ def test_config_row_subset(gpu, name):
     _check(gpu, wl, rows=sample_rows(wl.seq_len, extra=48, seed=wl.seed))
 
 
+@pytest.mark.parametrize("name", ["c4", "c5"])
+def test_config_every_row(gpu, name):
+    """The long-sequence configurations against the full oracle: every row of every slice (the
+    oracle runs threaded over (slice, row); c5 is ~5.5e11 flops, a few seconds on 16 host cores)."""
+    _check(gpu, CONFIGS[name])
+
+
 @pytest.mark.parametrize("wl", reference_smoke_cases(), ids=lambda w: w.name)
 def test_reference_smoke_cases(gpu, wl):
     """src/main.zig:196-287: O zero-initialised, abs tolerance 0.008 on the active region, the pad
