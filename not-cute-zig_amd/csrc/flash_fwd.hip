@@ -6,9 +6,10 @@
 // O = softmax(scale * Q K^T, causal mask) V per (batch, head) slice, f16 inputs, f32 accumulation,
 // f32 output, online softmax over key tiles with the row max/sum rescale of
 // src/flash_h64_bn32.zig:139-211 and the final O / l of src/flash_h64_bn32.zig:246-260. P is rounded
-// to f16 for the PV product; the generic kernels and most f16 pipelined ones sum the unrounded
-// weights as the reference does (src/flash_h64_bn32.zig:180-185), the q2s4, d=32 q4s1 and all bf16
-// pipelined kernels sum the rounded ones (numerator and denominator then use the same P).
+// to f16 for the PV product, and every kernel sums those rounded weights for l, so numerator and
+// denominator use the same P. (The reference sums the unrounded f32 weights,
+// src/flash_h64_bn32.zig:180-185, which biases O by up to 2^-11 |V| when the dominant weights round
+// the same way.)
 //
 // gfx950 formulation, common to both kernel families
 //   * One wave owns 32 queries. It computes the transposed score tile S^T = K * Q^T with
@@ -98,15 +99,13 @@ __device__ __forceinline__ float sum2(half2v p, float acc) {
         return __builtin_amdgcn_fdot2(p, ones, acc, false);
     }
 }
-// A 32-key tile's weight sum (per lane, 16 weights) at or above this moves the running max to the
-// tile max. f16: a weight that overflows f16 does; with the sum of the rounded weights (F32SUM
-// false) only that sum turns infinite, with the sum of the f32 weights (F32SUM true) a sum of 65504
-// or more is taken as the sign (a weight that rounds to infinity is at least 65520). bf16 has f32's
-// range, so weights are held below 2^20 to keep the f32 row sum and O accumulators far from
-// overflow.
-template <bool BF, bool F32SUM>
+// A 32-key tile's weight sum (per lane, 16 rounded weights) at or above this moves the running max
+// to the tile max. f16: a weight that overflows f16 does, which turns the sum of the rounded
+// weights infinite. bf16 has f32's range, so weights are held below 2^20 to keep the f32 row sum
+// and O accumulators far from overflow.
+template <bool BF>
 __device__ __forceinline__ float weight_sum_limit() {
-    return BF ? 1048576.0f : F32SUM ? 65504.0f : __builtin_inff();
+    return BF ? 1048576.0f : __builtin_inff();
 }
 
 // Position of key kk (block-relative) inside a staged V^T row: swap bits 2 and 3.
@@ -341,18 +340,13 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
         const float m_new = fmaxf(m, tmax);
         const float m_use = (m_new == neg_inf()) ? 0.f : m_new;  // fully masked so far: weights 0
         const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-        float psum = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            p[r] = __builtin_amdgcn_exp2f(p[r] - m_use);
-            psum += p[r];
-        }
-        l = l * alpha + psum;
-        m = m_new;
-#pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt) o[mt] *= alpha;
+        for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(p[r] - m_use);
 
+        // P rounded to the element type for the PV product; the row sum adds those rounded weights,
+        // so numerator and denominator carry the same rounding.
         half8 pf[2];
+        float psum = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -360,7 +354,12 @@ __device__ __forceinline__ void flash_fwd_body(const nc_flash_kernel_args &a) {
                 const half2v h = round2<BF>(p[8 * ks + j], p[8 * ks + j + 1]);
                 pf[ks][j] = h[0];
                 pf[ks][j + 1] = h[1];
+                psum = sum2<BF>(h, psum);
             }
+        l = l * alpha + psum;
+        m = m_new;
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt) o[mt] *= alpha;
 
         // O^T += V^T * P^T.
 #pragma unroll
@@ -741,19 +740,13 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // Log2-domain scale. A negative scale is applied by negating the resident Q operand (exact),
     // a zero scale by a tiny positive one (every score then rounds to weight exp2(0) = 1, as with
     // a zero scale), so the softmax below can assume sc > 0.
-    // Row sum of a tile: the f32 weights added by v_add_f32 (F32SUM), or the f16/bf16-rounded
-    // weights added by v_dot2c against 1.0 pairs. v_dot2c does not execute while an MFMA of the
-    // same SIMD is in flight (measured: 8 v_dot2c per 32x32x16 MFMA take longer than both run one
-    // after the other, where FMA, exp and the f16 packing hide the MFMAs entirely), so the f32 adds
-    // run faster, but keep 8 more VGPRs live. Interleaved A/B on MI355X: 1-1.7 % faster for the
-    // private-staging (q1s8) and d=64 one-split (q8s1, q4s1) kernels; the q2s4 kernels lose
-    // occupancy instead (d=16: 6 -> 5 waves per SIMD, 8.7 % slower; d=64: capped at the 128 VGPRs
-    // that let two workgroups share a CU, they spill) and d=32 q4s1 gains nothing, so those keep
-    // v_dot2c. With unrounded weights in the denominator, the rounding of P biases O by up to
-    // the rounding's relative error times |V| when the dominant weights round the same way: 2^-12
-    // for f16, but 2^-9 for bf16, which breaks the bf16 bar on such inputs, so bf16 always sums the
-    // rounded weights (numerator and denominator then use the same P and the bias cancels).
-    constexpr bool F32SUM = !BF && (NS == 8 || (D == 64 && NS == 1));
+    // Row sum of a tile: the weights exactly as rounded into P, added by v_dot2c against 1.0 pairs,
+    // so numerator and denominator carry the same rounding. (Dividing by the sum of the unrounded
+    // f32 weights, as the reference does, biases O by up to the rounding's relative error, 2^-11 for
+    // f16, times |V| whenever the dominant weights round the same way: 7.8e-3 at |V| = 16.)
+    // v_dot2c does not execute while an MFMA of the same SIMD is in flight (measured: 8 v_dot2c per
+    // 32x32x16 MFMA take longer than both run one after the other, where FMA, exp and the f16
+    // packing hide the MFMAs entirely), but it keeps the fewest registers live.
     float sc = a.scale * kLog2e;
     const bool neg_q = sc < 0.f;  // Q is negated once it has landed
     if (neg_q) sc = -sc;
@@ -795,8 +788,8 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
 
         // Online softmax (sc > 0). P = exp2(sc * s - m) is formed against the running max m as it
-        // stands and rounded to f16 for the PV product; the row sum adds the f32 weights or the
-        // rounded ones (F32SUM). f16 keeps its relative precision up to 65504, so m only has to
+        // stands and rounded to f16 for the PV product; the row sum adds the rounded weights.
+        // f16 keeps its relative precision up to 65504, so m only has to
         // move when some weight overflows f16, which shows in that lane's tile sum (see
         // weight_sum_limit); then (and while a row has no max yet)
         // the tile max is taken - before scaling, exact since rounding is monotonic - O and l
@@ -822,23 +815,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
         half8 pf[2];
         auto weights = [&]() {
-            if constexpr (F32SUM) {
-                float part[2];
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    float e[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[8 * ks + i], sc, neg_m));
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const half2v h = round2<BF>(e[2 * t], e[2 * t + 1]);
-                        pf[ks][2 * t] = h[0];
-                        pf[ks][2 * t + 1] = h[1];
-                    }
-                    part[ks] = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
-                }
-                return part[0] + part[1];
-            } else {
+            {
                 float ls = 0.f;
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
@@ -879,7 +856,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             ls = weights();
         } else {
             ls = weights();
-            if (__builtin_amdgcn_ballot_w64(!(ls < weight_sum_limit<BF, F32SUM>()))) {
+            if (__builtin_amdgcn_ballot_w64(!(ls < weight_sum_limit<BF>()))) {
                 to_tile_max();  // a weight overflowed (f16) or grew too large (bf16): redo the tile
                 ls = weights();
             }
@@ -1203,6 +1180,14 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
     }
 }
 
+// The per-symbol contract of the reference's kernels:
+//   ALWAYS_CAUSAL  the causal argument is ignored and the mask always applies
+//                  (flash_attention_fwd_h64_causal: `_ = causal`, src/flash_h64_causal.zig:34, and the
+//                  unconditional key_row <= q_row test of :113-118);
+//   D64_ONLY       head_dim != 64 returns without writing (src/flash_h64.zig:35,
+//                  src/flash_h64_bn32.zig:40, src/flash_h64_causal.zig:35); the other symbols accept
+//                  head_dim 16, 32 and 64 (src/flash_v2.zig:37, src/flash_opt.zig:31, src/kernels.zig:394).
+template <bool ALWAYS_CAUSAL, bool D64_ONLY>
 __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o,
                                                  uint64_t seq_len, uint64_t head_dim, uint64_t q_stride,
                                                  uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, float scale,
@@ -1211,12 +1196,15 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
     // Shapes the reference's kernels reject return without writing (src/flash_h64_bn32.zig:40).
     if (seq_len == 0 || seq_len > 0x7fffffffull || (blockDim.x & 63) || blockDim.x > 64 * kRefMaxWaves) return;
     const int S = (int)seq_len;
-    if (head_dim == 16)
-        flash_fwd_refabi_body<16>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, causal != 0, smem);
+    const bool cz = ALWAYS_CAUSAL || causal != 0;
+    if (head_dim == 64)
+        flash_fwd_refabi_body<64>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, cz, smem);
+    else if (D64_ONLY)
+        return;
+    else if (head_dim == 16)
+        flash_fwd_refabi_body<16>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, cz, smem);
     else if (head_dim == 32)
-        flash_fwd_refabi_body<32>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, causal != 0, smem);
-    else if (head_dim == 64)
-        flash_fwd_refabi_body<64>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, causal != 0, smem);
+        flash_fwd_refabi_body<32>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, cz, smem);
 }
 
 }  // namespace
@@ -1299,17 +1287,19 @@ NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_causal, 16, 1, 8, true, 2, 1)
 
 // Reference-ABI symbols (src/flash_v2.zig:23, src/flash_opt.zig:17, src/flash_h64.zig:21,
 // src/flash_h64_bn32.zig:26, src/flash_h64_causal.zig:20, src/kernels.zig:380): one body, launched
-// with the reference's grid (ceil(S/16), batch_heads) and 64 or 128 threads.
-#define NC_FLASH_REFABI_KERNEL(NAME)                                                                  \
+// with the reference's grid (ceil(S/16), batch_heads) and 64 or 128 threads; each symbol keeps its
+// reference kernel's head_dim domain and causal handling (flash_fwd_refabi's two switches).
+#define NC_FLASH_REFABI_KERNEL(NAME, ALWAYS_CAUSAL, D64_ONLY)                                         \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                           \
         const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t seq_len,          \
         uint64_t head_dim, uint64_t q_stride, uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, \
         float scale, uint32_t causal) {                                                               \
-        flash_fwd_refabi(q, k, v, o, seq_len, head_dim, q_stride, k_stride, v_stride, o_stride, scale, causal); \
+        flash_fwd_refabi<ALWAYS_CAUSAL, D64_ONLY>(q, k, v, o, seq_len, head_dim, q_stride, k_stride, v_stride, \
+                                                  o_stride, scale, causal);                          \
     }
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_v2)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_opt)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_bn32)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_causal)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_v2, false, false)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_opt, false, false)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64, false, true)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_bn32, false, true)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_causal, true, true)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd, false, false)

@@ -1,9 +1,21 @@
 """The reference's kernel symbols in the gfx950 code object (src/main_device.zig:19-47), launched
 the way the reference's own callers launch them (src/main.zig:822-840, 1024-1035): module
 getFunction by name, the 12 kernel parameters (88 bytes), grid (ceil(S/16), batch_heads), block =
-the reference's thread count (src/flash.zig:84-95). Parity against the oracle, pads untouched."""
+the reference's thread count (src/flash.zig:84-95).
+
+Each symbol is held to its reference kernel's contract, not to the dispatched path's:
+  - flash_attention_fwd_h64_causal ignores its `causal` argument and always masks
+    (`_ = causal`, src/flash_h64_causal.zig:34; mask key_row <= q_row, :113-118), so a launch with
+    causal = 0 must match the *causal* oracle;
+  - flash_attention_fwd_h64, _h64_bn32 and _h64_causal return without writing when head_dim != 64
+    (src/flash_h64.zig:35, src/flash_h64_bn32.zig:40, src/flash_h64_causal.zig:35): O stays
+    bit-identical to the sentinel it was filled with;
+  - flash_attention_fwd_v2, _opt and the legacy flash_attention_fwd accept head_dim 16, 32 and 64
+    (src/flash_v2.zig:37, src/flash_opt.zig:31, src/kernels.zig:394) and honour `causal`.
+Parity against the oracle, pads untouched."""
 
 import ctypes
+import dataclasses
 
 import numpy as np
 import pytest
@@ -17,6 +29,8 @@ pytestmark = pytest.mark.gpu
 # symbol -> threads per block in the reference (4 warps of 32 = 128, flash_warps = 2 -> 64)
 REF_KERNELS = {"flash_attention_fwd_v2": 128, "flash_attention_fwd_h64_bn32": 128, "flash_attention_fwd_h64": 64,
                "flash_attention_fwd_opt": 64, "flash_attention_fwd_h64_causal": 64, "flash_attention_fwd": 64}
+D64_ONLY = {"flash_attention_fwd_h64", "flash_attention_fwd_h64_bn32", "flash_attention_fwd_h64_causal"}
+ALWAYS_CAUSAL = {"flash_attention_fwd_h64_causal"}
 
 
 def launch_reference_way(mod, name, threads, wl, q, k, v, o_init):
@@ -35,11 +49,22 @@ def launch_reference_way(mod, name, threads, wl, q, k, v, o_init):
             b.free()
 
 
+def expected(name, wl, q, k, v, o_init):
+    """What the reference kernel `name` leaves in O: nothing written (None) outside its head_dim
+    domain, else the oracle with the kernel's effective causal flag."""
+    if name in D64_ONLY and wl.head_dim != 64:
+        return None, wl
+    eff = dataclasses.replace(wl, causal=True) if name in ALWAYS_CAUSAL else wl
+    return fc.oracle(eff, q, k, v, o_init=o_init), eff
+
+
 CASES = reference_smoke_cases() + reference_compare_cases()[::3] + [
     Workload("ra_neg_scale", 2, 45, 32, True, -0.4, (("normal", 0.0, 1.0),) * 3, seed=31),
     Workload("ra_s1", 3, 1, 64, False, 0.125, (("normal", 0.0, 1.0),) * 3, seed=32),
     Workload("ra_long", 2, 700, 64, True, 0.125, (("normal", 0.0, 2.0),) * 3, seed=33, q_stride=700 * 64 + 5),
+    Workload("ra_long_nc", 2, 300, 64, False, 0.125, (("normal", 0.0, 2.0),) * 3, seed=36),
     Workload("ra_d16", 4, 130, 16, False, 0.25, REFERENCE_FILLS, o_stride=130 * 16 + 3),
+    Workload("ra_d32_nc", 2, 96, 32, False, 0.2, (("normal", 0.0, 1.0),) * 3, seed=37),
 ]
 
 
@@ -50,10 +75,29 @@ def test_reference_symbol(gpu, name, wl):
     print(f"[case] {name} threads={threads} {wl.describe()}", flush=True)
     q, k, v = wl.make_inputs()
     o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
-    ref = fc.oracle(wl, q, k, v, o_init=o_init)
+    ref, eff = expected(name, wl, q, k, v, o_init)
     out = launch_reference_way(gpu, name, threads, wl, q, k, v, o_init)
-    fc.assert_parity(out, ref, fc.active_index(wl), f"{name}/{wl.name}")
-    fc.assert_pads_untouched(out, o_init, wl, f"{name}/{wl.name}")
+    if ref is None:
+        assert np.array_equal(out.view(np.uint32), o_init.view(np.uint32)), \
+            f"{name}/{wl.name}: head_dim {wl.head_dim} must leave O untouched"
+        return
+    fc.assert_parity(out, ref, fc.active_index(eff), f"{name}/{wl.name}")
+    fc.assert_pads_untouched(out, o_init, eff, f"{name}/{wl.name}")
+
+
+def test_h64_causal_ignores_causal_flag(gpu):
+    """causal = 0 and causal = 1 launches of flash_attention_fwd_h64_causal are bitwise equal, and
+    both differ from the non-causal oracle (the mask matters on this input)."""
+    wl = Workload("ra_flag", 2, 200, 64, False, 0.125, (("normal", 0.0, 1.0),) * 3, seed=38)
+    q, k, v = wl.make_inputs()
+    o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
+    out0 = launch_reference_way(gpu, "flash_attention_fwd_h64_causal", 64, wl, q, k, v, o_init)
+    out1 = launch_reference_way(gpu, "flash_attention_fwd_h64_causal", 64, dataclasses.replace(wl, causal=True),
+                                q, k, v, o_init)
+    assert np.array_equal(out0.view(np.uint32), out1.view(np.uint32))
+    ref_nc = fc.oracle(wl, q, k, v, o_init=o_init)
+    ea, _ = fc.errors(out0, ref_nc, fc.active_index(wl))
+    assert ea > 0.1, "the causal mask should change this output"
 
 
 def test_reference_symbol_other_block_sizes(gpu):
@@ -67,5 +111,6 @@ def test_reference_symbol_other_block_sizes(gpu):
     bad = Workload("ra_d48", 1, 40, 48, False, 0.1, (("normal", 0.0, 1.0),) * 3, seed=35)
     q, k, v = bad.make_inputs()
     o_init = np.full(bad.length("o"), fc.SENTINEL, dtype=np.float32)
-    out = launch_reference_way(gpu, "flash_attention_fwd_opt", 64, bad, q, k, v, o_init)
-    assert np.array_equal(out.view(np.uint32), o_init.view(np.uint32))
+    for name in sorted(REF_KERNELS):
+        out = launch_reference_way(gpu, name, 64, bad, q, k, v, o_init)
+        assert np.array_equal(out.view(np.uint32), o_init.view(np.uint32)), name
