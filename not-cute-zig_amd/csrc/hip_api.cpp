@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 
@@ -24,6 +25,10 @@ struct nc_function_st {
 
 struct nc_module_st {
     hipModule_t mod = nullptr;
+    // Guards `functions`: several host threads may launch through one module (hipModuleGetFunction,
+    // the lookup the cache saves, is itself thread-safe). Entries are never removed before unload,
+    // so a returned nc_function stays valid without the lock.
+    std::mutex lock;
     std::unordered_map<std::string, std::unique_ptr<nc_function_st>> functions;
 };
 
@@ -195,6 +200,7 @@ int nc_module_unload(nc_module module) {
 int nc_module_get_function(nc_function *out, nc_module module, const char *name) {
     if (!out || !module || !name) return fail(NC_ERROR_INVALID_VALUE, "nc_module_get_function: null argument");
     *out = nullptr;
+    std::lock_guard<std::mutex> guard(module->lock);
     auto it = module->functions.find(name);
     if (it != module->functions.end()) {
         *out = it->second.get();

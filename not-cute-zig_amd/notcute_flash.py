@@ -551,11 +551,26 @@ def flash_launch(module: Module, q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuff
                  k_len: Optional[int] = None, v_len: Optional[int] = None, o_len: Optional[int] = None,
                  q_offset: int = 0, k_offset: int = 0, v_offset: int = 0, o_offset: int = 0) -> None:
     """flash.launch (src/flash.zig:31-70). Lengths are in elements and default to the buffer size;
-    offsets (in elements) let a caller pass a sub-slice, e.g. a deliberately misaligned base."""
-    ql = q.nbytes // 2 - q_offset if q_len is None else q_len
-    kl = k.nbytes // 2 - k_offset if k_len is None else k_len
-    vl = v.nbytes // 2 - v_offset if v_len is None else v_len
-    ol = o.nbytes // 4 - o_offset if o_len is None else o_len
+    offsets (in elements) let a caller pass a sub-slice, e.g. a deliberately misaligned base.
+
+    Raises ValueError, before anything is launched, when an offset is negative or past the end of
+    its buffer, or a length is negative or longer than the elements left after the offset: the C
+    ABI's short-buffer check (requireLen) can only trust lengths that describe real memory, and a
+    negative one would wrap to ~2^64 in size_t."""
+    def span(name, buf, esize, offset, length):
+        avail = buf.nbytes // esize
+        if offset < 0 or offset > avail:
+            raise ValueError(f"flash_launch: {name}_offset {offset} outside the {avail}-element buffer")
+        n = avail - offset if length is None else length
+        if n < 0 or n > avail - offset:
+            raise ValueError(f"flash_launch: {name}_len {n} does not fit the {avail - offset} elements "
+                             f"after offset {offset}")
+        return n
+
+    ql = span("q", q, 2, q_offset, q_len)
+    kl = span("k", k, 2, k_offset, k_len)
+    vl = span("v", v, 2, v_offset, v_len)
+    ol = span("o", o, 4, o_offset, o_len)
     check(lib().nc_flash_launch_async(module.handle, q.ptr + 2 * q_offset, ql, k.ptr + 2 * k_offset, kl,
                                       v.ptr + 2 * v_offset, vl, o.ptr + 4 * o_offset, ol, ctypes.byref(opts),
                                       stream), "flash.launch")

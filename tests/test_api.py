@@ -224,6 +224,31 @@ def test_launch_validates_before_touching_the_module():
     assert nc.STATUS_NAMES[st] == "InvalidValue"
 
 
+class _FakeBuffer:
+    """Stands in for a DeviceBuffer: flash_launch only reads .ptr and .nbytes before the C call."""
+
+    def __init__(self, nbytes):
+        self.ptr = 0x10000
+        self.nbytes = nbytes
+
+
+@pytest.mark.parametrize("kw", [
+    {"q_offset": -1}, {"k_offset": 513}, {"o_offset": 600},          # offsets outside the buffer
+    {"v_len": -5}, {"q_len": 513}, {"o_offset": 10, "o_len": 503},   # lengths past what is left
+])
+def test_python_launch_rejects_bad_offsets_and_lengths(kw):
+    """A negative or oversized length would wrap in size_t and defeat requireLen; the binding raises
+    ValueError before anything reaches the C ABI (the fake module handle would fail there)."""
+    q, k, v = _FakeBuffer(512 * 2), _FakeBuffer(512 * 2), _FakeBuffer(512 * 2)
+    o = _FakeBuffer(512 * 4)
+
+    class _Mod:
+        handle = None
+
+    with pytest.raises(ValueError):
+        nc.flash_launch(_Mod(), q, k, v, o, nc.options(batch_heads=2, seq_len=16, head_dim=16), **kw)
+
+
 def test_work_model_matches_reference_formulas():
     w = nc.work_model(CONFIGS["c3"].options())
     assert w.flops_reference == 1_074_790_400  # BH*4*S(S+1)/2*d, src/main.zig:1032-1033
