@@ -5,11 +5,14 @@ One step = one flash-attention forward of the headline workload (BH=8 S=1024 d=6
 f32 out) with Q/K/V already resident in HBM. Launches go through the C ABI (nc_flash_launch_async)
 on one stream; the timed region replays a HIP graph of back-to-back launches, bracketed by HIP
 events on that stream and a device synchronize on both sides, so the average per step is the
-kernel's average duration plus the (small) inter-kernel gap.
+kernel's average duration plus the (small) inter-kernel gap. Before it: --warmup untimed steps and
+a wall-clock settle phase (--settle-ms) of replays of the same graph, so that a short --warmup does
+not time a GPU that is still raising its clock.
 
 Prints ONE JSON line (rank 0, N=1) with the metric of the benchmark plan, a `roofline` object for
-the flash kernel, and a `cpu_baseline` object: the CPU oracle (a port of the reference's scalar CPU
-reference) timed on this host on the same workload.
+the flash kernel, a `cpu_baseline` object (the CPU oracle, a port of the reference's scalar CPU
+reference, timed on this host on the same workload) and `extra_workloads`: the long-sequence
+configurations c4 and c5 timed the same way, each with its own parity check.
 """
 
 from __future__ import annotations
@@ -111,14 +114,117 @@ def calibrate_copy(mod: nc.Module, stream: nc.Stream, nbytes: int, iters: int) -
     log(f"calibration copy: {iters} x {n16 * 16} bytes read + written")
 
 
+def time_graph(stream, launch, steps: int, warmup: int, graph_batch: int, settle_ms: float) -> dict:
+    """Time exactly `steps` launches issued as replays of a HIP graph of back-to-back launches,
+    between HIP events on the launch stream with a device synchronize on both sides.
+
+    Before the timed region: `warmup` untimed steps as replays of the same graph, then a clock-settle
+    phase that keeps replaying it until `settle_ms` of wall time have passed (a GPU that has idled
+    runs its first milliseconds of work on a lower clock, and a short --warmup alone would time
+    that). At most 10 graphs are queued between synchronizes: under rocprofv3's kernel tracer, about
+    200 queued graphs of 100 launches each made the host runtime abort."""
+    gb = max(1, min(graph_batch, steps))
+    full, rest = divmod(steps, gb)
+    graph = nc.Graph.capture(stream, lambda: [launch() for _ in range(gb)])
+    tail = nc.Graph.capture(stream, lambda: [launch() for _ in range(rest)]) if rest else None
+    for i in range(warmup // gb):
+        graph.launch(stream)
+        if i % 10 == 9:
+            stream.synchronize()
+    stream.synchronize()
+    t0 = time.perf_counter()
+    settle_graphs = 0
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        for _ in range(10):
+            graph.launch(stream)
+        settle_graphs += 10
+        stream.synchronize()
+    settled = (time.perf_counter() - t0) * 1e3
+    ev0, ev1 = nc.Event(), nc.Event()
+    nc.synchronize()
+    # Two untimed replays queued ahead of the start event keep the GPU busy while the host submits
+    # the timed graphs, so the event pair brackets the K launches themselves rather than the host's
+    # submission latency of the first timed graph (with K = 20 that was ~1.5 us of every step).
+    graph.launch(stream)
+    graph.launch(stream)
+    ev0.record(stream.handle)
+    for i in range(full):
+        graph.launch(stream)
+    if tail is not None:
+        tail.launch(stream)
+    ev1.record(stream.handle)
+    ev1.synchronize()
+    nc.synchronize()
+    total_ms = nc.Event.elapsed(ev0, ev1)
+    graph.destroy()
+    if tail is not None:
+        tail.destroy()
+    ev0.destroy()
+    ev1.destroy()
+    return {"ms_per_step": total_ms / steps, "total_ms": total_ms, "steps": steps,
+            "settle_ms": round(settled, 1), "settle_launches": settle_graphs * gb}
+
+
+def measure_extra(mod, name: str, args) -> dict:
+    """One more workload (c4 / c5: the MFMA-bound configurations) timed exactly like the headline,
+    with its own parity check on sampled query rows. Reported as extra keys of the one JSON line."""
+    wl = CONFIGS[name]
+    if args.dtype != wl.dtype:
+        wl = dataclasses.replace(wl, dtype=args.dtype)
+    opts = wl.options()
+    work = wl.work()
+    sel = nc.select_kernel(opts)
+    q, k, v = wl.make_inputs()
+    dq, dk, dv = (nc.DeviceBuffer.from_array(x) for x in (q, k, v))
+    do = nc.DeviceBuffer(wl.length("o") * 4)
+    do.memset(0)
+    stream = nc.Stream()
+    try:
+        def launch():
+            nc.flash_launch(mod, dq, dk, dv, do, opts, stream=stream.handle)
+
+        launch()
+        stream.synchronize()
+        max_abs = None
+        if not args.no_verify:
+            import flashcheck  # noqa: E402  (checker only)
+
+            rows = np.arange(0, wl.seq_len, 97)
+            ref = flashcheck.oracle(wl, q, k, v, rows=rows)
+            max_abs, max_rel = flashcheck.errors(do.download(np.float32, wl.length("o")), ref,
+                                                 flashcheck.active_index(wl, rows))
+            bar_abs, bar_rel = flashcheck.parity_bar(wl.dtype)
+            if not (max_abs <= bar_abs and max_rel <= bar_rel):
+                raise RuntimeError(f"{name}: parity failure max-abs {max_abs} max-rel {max_rel}")
+        t = time_graph(stream, launch, args.steps, args.warmup, args.graph_batch, args.settle_ms)
+        tflops = work["flops"] / (t["ms_per_step"] * 1e-3) / 1e12
+        log(f"bench: {wl.describe()} -> {sel.name.decode()}: {t['ms_per_step'] * 1e3:.2f} us/step, "
+            f"{tflops:.1f} TFLOP/s ({100 * tflops / PEAK_F16_TFLOPS:.2f} % of f16 peak), parity max-abs {max_abs}")
+        return {"workload": f"{wl.name}: BH={wl.batch_heads} S={wl.seq_len} d={wl.head_dim} "
+                            f"{'causal' if wl.causal else 'non-causal'}, Q/K/V {wl.dtype} {describe_dists(wl.dists)} "
+                            f"seed {wl.seed}, scale {wl.scale:g}",
+                "kernel": sel.name.decode(), "ms_per_step": round(t["ms_per_step"], 6), "steps": t["steps"],
+                "settle_ms": t["settle_ms"], "tflops": round(tflops, 2),
+                "pct_f16_mfma_peak": round(100.0 * tflops / PEAK_F16_TFLOPS, 3), "flops_per_step": work["flops"],
+                "parity_max_abs": max_abs, "parity_rows": "every 97th query row of every slice"}
+    finally:
+        for b in (dq, dk, dv, do):
+            b.free()
+        stream.destroy()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000, help="timed steps (flash launches)")
-    ap.add_argument("--warmup", type=int, default=20000,
-                    help="untimed warmup steps: up to 50 eager launches, the rest graph replays (clock ramp)")
+    ap.add_argument("--warmup", type=int, default=5000,
+                    help="untimed warmup steps: up to 50 eager launches, the rest graph replays")
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(CONFIGS))
     ap.add_argument("--graph-batch", type=int, default=100, help="launches captured per HIP graph")
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="untimed clock-settle replays of the timed graph, in wall-clock ms, after --warmup")
+    ap.add_argument("--extra", default="c4,c5",
+                    help="comma-separated extra workloads timed the same way (extra keys of the JSON line; '' for none)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget (0: skip)")
     ap.add_argument("--ref-iters", type=int, default=20, help="iterations of the per-launch event timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -188,58 +294,32 @@ def main() -> int:
                                bytes_=work["bytes"], flops=work["flops_reference"], stream=stream.handle)
 
     # timed region: graphs of back-to-back launches
-    gb = max(1, min(args.graph_batch, args.steps))
-    reps = max(1, args.steps // gb)
-    steps = gb * reps
-    graph = nc.Graph.capture(stream, lambda: [launch() for _ in range(gb)])
-    # warmup, part 2: the remaining warmup steps as replays of the timed graph, so the timed region
-    # starts at the clock the GPU holds under this load (a GPU that has idled runs its first
-    # milliseconds of work on a lower clock). At most 10 graphs are in flight between synchronizes:
-    # under rocprofv3's kernel tracer, ~200 queued graphs of 100 launches crashed the host runtime.
-    for i in range(max(1, (args.warmup - eager_warmup) // gb)):
-        graph.launch(stream)
-        if i % 10 == 9:
-            stream.synchronize()
-    stream.synchronize()
-    ev0, ev1 = nc.Event(), nc.Event()
-    nc.synchronize()
-    ev0.record(stream.handle)
-    for _ in range(reps):
-        graph.launch(stream)
-    ev1.record(stream.handle)
-    ev1.synchronize()
-    nc.synchronize()
-    total_ms = nc.Event.elapsed(ev0, ev1)
-    ms = total_ms / steps
-    graph.destroy()
-    log(f"bench: {steps} steps in {total_ms:.3f} ms -> {ms * 1e3:.3f} us/step; per-launch event timing "
-        f"mean {per_launch.mean_ms * 1e3:.2f} us min {per_launch.min_ms * 1e3:.2f} us")
+    t = time_graph(stream, launch, args.steps, args.warmup - eager_warmup, args.graph_batch, args.settle_ms)
+    ms, steps = t["ms_per_step"], t["steps"]
+    log(f"bench: {steps} steps in {t['total_ms']:.3f} ms -> {ms * 1e3:.3f} us/step (after {t['settle_ms']:.0f} ms "
+        f"of clock-settle replays); per-launch event timing mean {per_launch.mean_ms * 1e3:.2f} us "
+        f"min {per_launch.min_ms * 1e3:.2f} us")
 
     # One event pair around 100 plain back-to-back launches (no graph), divided by 100.
     for _ in range(10):
         launch()
     stream.synchronize()
+    ev0, ev1 = nc.Event(), nc.Event()
     ev0.record(stream.handle)
     for _ in range(100):
         launch()
     ev1.record(stream.handle)
     ev1.synchronize()
     b2b_ms = nc.Event.elapsed(ev0, ev1) / 100
+    ev0.destroy()
+    ev1.destroy()
     log(f"bench: 100 back-to-back launches without a graph: {b2b_ms * 1e3:.3f} us/launch")
 
     # Fixed per-launch cost: an empty kernel with the same grid and block, replayed the same way.
     empty = mod.get_function("nc_util_empty")
-    egraph = nc.Graph.capture(stream, lambda: [empty.launch(tuple(sel.grid), (sel.threads,), [ka],
-                                                            stream=stream.handle) for _ in range(gb)])
-    egraph.launch(stream)
-    stream.synchronize()
-    ev0.record(stream.handle)
-    for _ in range(reps):
-        egraph.launch(stream)
-    ev1.record(stream.handle)
-    ev1.synchronize()
-    floor_ms = nc.Event.elapsed(ev0, ev1) / steps
-    egraph.destroy()
+    tf_ = time_graph(stream, lambda: empty.launch(tuple(sel.grid), (sel.threads,), [ka], stream=stream.handle),
+                     steps, 0, args.graph_batch, min(args.settle_ms, 50.0))
+    floor_ms = tf_["ms_per_step"]
     log(f"bench: empty kernel with the same grid: {floor_ms * 1e3:.3f} us/launch")
 
     if args.calibrate_copy:
@@ -264,6 +344,11 @@ def main() -> int:
     else:
         roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(tflops / PEAK_F16_TFLOPS, 5), "traffic": traffic}
+
+    extra = {}
+    for name in filter(None, (x.strip() for x in args.extra.split(","))):
+        if name != wl.name:
+            extra[name] = measure_extra(mod, name, args)
 
     cpu = cpu_all = None
     if args.cpu_seconds > 0:
@@ -299,7 +384,10 @@ def main() -> int:
         "flops_per_step": work["flops"],
         "flops_per_step_reference_formula": work["flops_reference"],
         "bytes_per_step": work["bytes"],
-        "timing": "HIP events around graph replays of back-to-back launches on the launch stream",
+        "timing": "HIP events around graph replays of back-to-back launches on the launch stream, after "
+                  "--warmup replays and a wall-clock settle phase of replays",
+        "settle_ms": t["settle_ms"],
+        "settle_launches": t["settle_launches"],
         "per_launch_event_ms": {"mean": per_launch.mean_ms, "min": per_launch.min_ms, "max": per_launch.max_ms,
                                 "iters": args.ref_iters},
         "back_to_back_launch_ms": round(b2b_ms, 6),
@@ -310,6 +398,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "cpu_baseline_threads": cpu_all,
+        "extra_workloads": extra,
     }
     print(json.dumps(rec), flush=True)
     for b in (dq, dk, dv, do):
