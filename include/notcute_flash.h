@@ -13,8 +13,11 @@
  *   - All functions return an nc_status (0 = success) unless stated otherwise.
  *   - Device buffers are plain pointers plus element counts; no C++ or torch types cross the ABI.
  *   - Q/K/V are IEEE binary16 stored as uint16_t bit patterns, O is float32.
- *   - Like the reference, launches are asynchronous and allocate nothing; results become visible
- *     after a synchronising copy or an nc_stream_synchronize / nc_device_synchronize.
+ *   - Like the reference, launches are asynchronous; results become visible after a synchronising
+ *     copy or an nc_stream_synchronize / nc_device_synchronize. A launch allocates nothing, except
+ *     that the first launch on a module whose kernel needs scratch memory (the pair-split kernels:
+ *     selection.scratch_bytes > 0) allocates the module's workspace, kept until nc_module_unload;
+ *     nc_flash_reserve_workspace allocates it ahead of time (e.g. before a graph capture).
  *   - One process, one GPU (device 0), one calling thread, as in the reference.
  *
  * The same header is included by the device code (flash_fwd.hip) for the kernel argument block.
@@ -227,6 +230,7 @@ typedef struct nc_flash_kernel_selection {
     uint32_t kv_splits;         /* waves that share one query tile and split its keys */
     uint32_t lds_bytes;         /* static LDS of the kernel */
     uint32_t aligned;           /* 1: 16-byte vector path, 0: element-wise path for odd strides */
+    uint64_t scratch_bytes;     /* device scratch the kernel needs (pair-split kernels), else 0 */
 } nc_flash_kernel_selection;
 
 /* selectKernel (src/flash.zig:78-96), re-tuned for MI355X. Assumes 16-byte aligned base pointers
@@ -262,9 +266,22 @@ typedef struct nc_flash_kernel_args {
     uint64_t o_row_stride;
     uint32_t batch_heads;
     uint32_t num_q_blocks; /* ceil(seq_len / block_m) */
-    uint32_t reserved0;
-    uint32_t reserved1;
+    void *scratch;         /* device scratch of kernels that need one (selection.scratch_bytes), else NULL */
 } nc_flash_kernel_args;
+
+/* Layout of the scratch of the pair-split kernels (selection.scratch_bytes): a fixed region of
+ * NC_XS_COUNTER_BYTES holding one u32 exchange counter per pair of workgroups (at most
+ * NC_XS_MAX_PAIRS = batch_heads * (ceil(seq_len/32) / 2) pairs), then two slots per pair of
+ * 32 x head_dim f32 partial outputs plus 32 (max, sum) f32 pairs. The counter region is the same for
+ * every shape, so shapes that share a workspace never see each other's partial data as counters;
+ * the counters must start at zero (even) and every launch leaves them even. */
+#define NC_XS_COUNTER_BYTES 65536u
+#define NC_XS_MAX_PAIRS (NC_XS_COUNTER_BYTES / 4u)
+
+/* Scratch bytes the kernel `name` needs for a launch with these options (0 for every kernel but the
+ * pair-split ones), for callers that launch a kernel by name with their own scratch buffer, which
+ * must be zeroed before its first use. NC_ERROR_NOT_FOUND for a name that is not a flash kernel. */
+int nc_flash_kernel_scratch_bytes(const char *name, const nc_flash_options *opts, uint64_t *bytes);
 
 /* Fill the argument block for `sel` (row strides resolved, num_q_blocks derived). */
 int nc_flash_pack_args(const nc_flash_options *opts, const nc_flash_kernel_selection *sel,
@@ -276,10 +293,19 @@ int nc_flash_pack_args(const nc_flash_options *opts, const nc_flash_kernel_selec
  * kernel up in `module`, launch on the default stream. Asynchronous; allocates nothing. */
 int nc_flash_launch(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
                     const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts);
-/* Same on an explicit stream (a strict superset: the reference always uses the null stream). */
+/* Same on an explicit stream (a strict superset: the reference always uses the null stream).
+ * Launches whose kernel uses the module's workspace (selection.scratch_bytes > 0) must not overlap
+ * in time with another such launch on the same module (e.g. on two streams): they share it. */
 int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k,
                           size_t k_len, const uint16_t *v, size_t v_len, float *o, size_t o_len,
                           const nc_flash_options *opts, nc_stream stream);
+
+/* Extension (no counterpart in the reference, whose kernels use no scratch memory): make the
+ * module's workspace large enough for a launch with these options, allocating it now (device memory,
+ * zeroed), so that later launches allocate nothing. Stores the workspace in *workspace (may be NULL)
+ * for callers that launch the selected kernel themselves: they put it in nc_flash_kernel_args.scratch.
+ * Stores NULL, allocating nothing, when the selected kernel needs no scratch. */
+int nc_flash_reserve_workspace(nc_module module, const nc_flash_options *opts, void **workspace);
 
 /* Work model of one launch: flops and bytes as the reference's harness counts them
  * (src/main.zig:843-845, 1032-1034: causal keys = S(S+1)/2), and the half-square causal count

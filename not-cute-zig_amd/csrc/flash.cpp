@@ -18,6 +18,9 @@
 
 #include "notcute_flash.h"
 
+// hip_api.cpp: the module's workspace, grown (and zeroed) on demand.
+extern "C" int nc_internal_module_workspace(nc_module module, size_t bytes, void **out);
+
 namespace {
 
 // Kernel families of flash_fwd.hip. Geometry and LDS sizes must agree with Cfg<> / PipeCfg<>.
@@ -34,6 +37,7 @@ struct Variant {
     bool aligned;
     Family family;
     bool bf16;  // the `_bf16` twin of the kernel (bf16 Q/K/V)
+    bool xsplit = false;  // causal query blocks p and nqb-1-p shared by two workgroups (`x` kernels)
 
     uint32_t bm() const { return 32 * nq; }
     uint32_t bn() const { return 32 * ns * sub; }
@@ -44,7 +48,9 @@ struct Variant {
         if (family == Family::kPipe) {
             const uint32_t ring = nstage * 2 * bn() * d * 2;
             // + (m, l) area, + the workgroup's Q tile when key-split waves share it
-            return (ring > o_bytes ? ring : o_bytes) + nw * 32 * 2 * 4 + (ns > 1 ? bm() * d * 2 : 0);
+            // (+ a second Q tile and two exchange words for the pair-split kernels)
+            return (ring > o_bytes ? ring : o_bytes) + nw * 32 * 2 * 4 + (ns > 1 ? bm() * d * 2 : 0) +
+                   (xsplit ? bm() * d * 2 + 16 : 0);
         }
         const uint32_t dv = d < 32 ? 32 : d;
         const uint32_t stage = bn() * (d + 8) * 2 + dv * (bn() + 8) * 2;
@@ -54,6 +60,8 @@ struct Variant {
 
 #define PIPE(D, NQ, NS, P, C, T, BF) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "_" C T, D, NQ, NS, P, 1, \
                                       C[0] == 'c', true, Family::kPipe, BF}
+// Pair split (flash_fwd.hip's XS kernels): d=64 causal, one query wave, eight key splits.
+#define PIPEX(D, T, BF) {"nc_flash_fwd_d" #D "_q1s8p2x_causal" T, D, 1, 8, 2, 1, true, true, Family::kPipe, BF, true}
 // Two 32-key sub-tiles per wave per block ("t2": 32*NS*2 keys per block).
 #define PIPE2(D, NQ, NS, P, C, T, BF) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "t2_" C T, D, NQ, NS, P, 2, \
                                        C[0] == 'c', true, Family::kPipe, BF}
@@ -71,19 +79,34 @@ struct Variant {
     GEN(32, "causal", true, "", T, BF), GEN(64, "full", true, "", T, BF), GEN(64, "causal", true, "", T, BF),   \
     GEN(16, "full", false, "_unaligned", T, BF), GEN(16, "causal", false, "_unaligned", T, BF),                \
     GEN(32, "full", false, "_unaligned", T, BF), GEN(32, "causal", false, "_unaligned", T, BF),                \
-    GEN(64, "full", false, "_unaligned", T, BF), GEN(64, "causal", false, "_unaligned", T, BF)
+    GEN(64, "full", false, "_unaligned", T, BF), GEN(64, "causal", false, "_unaligned", T, BF), PIPEX(64, T, BF)
 
 const Variant kVariants[] = {VARIANTS("", false), VARIANTS("_bf16", true)};
 #undef VARIANTS
 #undef PIPE
 #undef PIPE2
+#undef PIPEX
 #undef GEN
 
 const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal, bool bf16) {
     for (const auto &v : kVariants)
-        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.causal == causal && v.bf16 == bf16)
+        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.causal == causal && v.bf16 == bf16 &&
+            !v.xsplit)
             return &v;
     return nullptr;
+}
+
+const Variant *find_xsplit(uint32_t d, bool bf16) {
+    for (const auto &v : kVariants)
+        if (v.xsplit && v.d == d && v.bf16 == bf16) return &v;
+    return nullptr;
+}
+
+// Pairs of workgroups of a pair-split launch, and its scratch: the fixed counter region, then two
+// slots per pair of 32 x d f32 partial O plus 32 (m, l) pairs (flash_fwd.hip's pair exchange).
+uint64_t xsplit_pairs(uint64_t batch_heads, uint64_t seq_len) { return batch_heads * (((seq_len + 31) / 32) / 2); }
+uint64_t xsplit_scratch_bytes(uint64_t batch_heads, uint64_t seq_len, uint64_t d) {
+    return NC_XS_COUNTER_BYTES + xsplit_pairs(batch_heads, seq_len) * 2 * (32 * d * 4 + 32 * 8);
 }
 
 const Variant *find_generic(uint32_t d, bool causal, bool aligned, bool bf16) {
@@ -132,7 +155,9 @@ const Variant *choose_pipe(const nc_flash_options &o) {
         if (causal) {
             if (wgs(256) >= 512 && (S <= 4096 || wgs(256) >= 1024)) return find_pipe(d, 8, 1, causal, bf);
             if (S <= 512 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal, bf);
-            if (wgs(64) >= (S <= 1024 ? 256u : 512u)) return find_pipe(d, 2, 4, causal, bf);
+            const uint64_t w64 = wgs(64);
+            if ((S <= 1024 && w64 >= 256) || (S <= 2048 && w64 >= 288) || (S <= 4096 && w64 >= 384) || w64 >= 512)
+                return find_pipe(d, 2, 4, causal, bf);
             return find_pipe(d, 1, 8, causal, bf);
         }
         if (S <= 256 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal, bf);
@@ -178,6 +203,18 @@ int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selec
                            ? choose_pipe(o)
                            : find_generic((uint32_t)d, o.causal != 0, aligned, o.element_type == NC_ELEMENT_BF16);
     if (!v) return NC_ERROR_NOT_FOUND;
+    // Long causal sequences over few heads on the private-staging kernel: pair the light and heavy
+    // query blocks so that every workgroup takes about half the heaviest block's keys. It pays once
+    // the whole grid runs at once (one workgroup per CU) and the heaviest block is long enough to
+    // outweigh the ~1.2 us exchange between the two workgroups of a pair: measured on MI355X,
+    // BH=1 S=8192 23.4 -> 18.6 us, BH=2 S=4096 13.4 -> 12.3 us, but c3 (32 query blocks) 5.9 -> 7.5 us
+    // and grids beyond 256 workgroups slower too.
+    const uint64_t nqb32 = (o.seq_len + 31) / 32;
+    if (v->family == Family::kPipe && v->causal && v->nq == 1 && v->d == 64 && nqb32 >= 96 &&
+        nqb32 * o.batch_heads <= 256 && xsplit_pairs(o.batch_heads, o.seq_len) <= NC_XS_MAX_PAIRS) {
+        const Variant *x = find_xsplit(v->d, v->bf16);
+        if (x) v = x;
+    }
     const uint64_t nqb = (o.seq_len + v->bm() - 1) / v->bm();
     uint64_t grid = 0;
     if (mul_overflows(nqb, o.batch_heads, &grid) || grid > 0xffffffffull) return NC_ERROR_OVERFLOW;
@@ -194,6 +231,7 @@ int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selec
     out->kv_splits = v->ns;
     out->lds_bytes = v->lds_bytes();
     out->aligned = aligned ? 1u : 0u;
+    out->scratch_bytes = v->xsplit ? xsplit_scratch_bytes(o.batch_heads, o.seq_len, d) : 0;
     return NC_SUCCESS;
 }
 
@@ -292,6 +330,10 @@ int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, con
     nc_flash_kernel_args args;
     st = nc_flash_pack_args(opts, &sel, q, k, v, o, &args);
     if (st) return st;
+    if (sel.scratch_bytes) {
+        st = nc_internal_module_workspace(module, sel.scratch_bytes, &args.scratch);
+        if (st) return st;
+    }
     nc_launch_config cfg;
     std::memset(&cfg, 0, sizeof cfg);
     cfg.grid[0] = sel.grid[0];
@@ -309,6 +351,30 @@ int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, con
 int nc_flash_launch(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
                     const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts) {
     return nc_flash_launch_async(module, q, q_len, k, k_len, v, v_len, o, o_len, opts, nullptr);
+}
+
+int nc_flash_kernel_scratch_bytes(const char *name, const nc_flash_options *opts, uint64_t *bytes) {
+    if (!name || !opts || !bytes) return NC_ERROR_INVALID_VALUE;
+    *bytes = 0;
+    for (const auto &v : kVariants)
+        if (std::strcmp(v.name, name) == 0) {
+            if (v.xsplit) *bytes = xsplit_scratch_bytes(opts->batch_heads, opts->seq_len, v.d);
+            return NC_SUCCESS;
+        }
+    return NC_ERROR_NOT_FOUND;
+}
+
+int nc_flash_reserve_workspace(nc_module module, const nc_flash_options *opts, void **workspace) {
+    if (workspace) *workspace = nullptr;
+    if (!module) return NC_ERROR_INVALID_VALUE;
+    nc_flash_kernel_selection sel;
+    int st = nc_flash_select_kernel(opts, &sel);
+    if (st) return st;
+    if (!sel.scratch_bytes) return NC_SUCCESS;
+    void *ws = nullptr;
+    st = nc_internal_module_workspace(module, sel.scratch_bytes, &ws);
+    if (!st && workspace) *workspace = ws;
+    return st;
 }
 
 int nc_flash_work_model(const nc_flash_options *opts, nc_flash_work *out) {

@@ -134,6 +134,26 @@ __device__ __forceinline__ void store_o(floatx4 *p, floatx4 v) {
     asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(p), "v"(v) : "memory");
 }
 
+// Agent-scope (sc1) accesses for the pair exchange between workgroups: coherent across the
+// device's XCDs, whose L2 caches are not coherent with one another for ordinary accesses, and
+// without the L2 writeback / invalidate that an agent-scope fence costs (buffer_wbl2 / buffer_inv).
+// Ordering comes from s_waitcnt: a partial's stores have completed before the counter increment
+// that announces them, and the partner's partial is loaded only after the counter showed it.
+// Measured on MI355X with partners on the same and on different XCDs: every merged value correct.
+__device__ __forceinline__ void store_agent(float *p, floatx4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_agent(float *p, float2v v) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+// Both loads issued, then waited for (asm loads are not tracked by the compiler's waits).
+__device__ __forceinline__ void load_agent(const float *p4, const float *p2, floatx4 &v4, float2v &v2) {
+    asm volatile("global_load_dwordx4 %0, %2, off sc1\n\tglobal_load_dwordx2 %1, %3, off sc1\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(v4), "=&v"(v2)
+                 : "v"(p4), "v"(p2)
+                 : "memory");
+}
+
 template <bool VEC>
 __device__ __forceinline__ void store4(float *p, floatx4 v) {
     if constexpr (VEC) {
@@ -613,14 +633,19 @@ struct PipeCfg {
     static constexpr int MT = D < 32 ? 1 : D / 32;
 };
 
-template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB, bool BF>
+template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB, bool BF, bool XS = false>
 __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &a) {
     using C = PipeCfg<D, NQ, NS, NSTAGE, SUB>;
     using SW = Swz<D>;
     static_assert(NSTAGE >= 1 && NSTAGE <= 8, "ring depth");
-    __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+    static_assert(!XS || (NQ == 1 && NS == 8 && SUB == 1 && CAUSAL), "pair split: causal private staging");
+    // XS: a second Q tile (the B workgroup's second query block) and two words for the pair exchange.
+    constexpr int XS_Q2 = C::LDS_BYTES;
+    constexpr int XS_WORDS = XS_Q2 + C::BM * D * 2;
+    __shared__ __attribute__((aligned(16))) char smem[XS ? XS_WORDS + 16 : C::LDS_BYTES];
 
     if (a.head_dim != (uint64_t)D || a.seq_len == 0) return;
+    if (XS && a.scratch == nullptr) return;  // the host always passes the pair-exchange buffer
 
     const int S = (int)a.seq_len;
     const uint32_t bh = a.batch_heads;
@@ -644,7 +669,58 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     const int hh = lane >> 5;
     const int qg = w / NS;
     const int s = w % NS;
-    const int q0 = qb * C::BM;
+
+    // Pair split (XS, causal private staging): the query blocks p and q = nqb-1-p of a head
+    // (p < nqb/2) hold nqb+1 key tiles (32 keys each) between them, and are shared by two
+    // workgroups so that neither takes more than about half the heaviest block's tiles.
+    //   A (slot 2p):   block q, key tiles [0, kA), kA = ceil(nqb/2): a partial (m, l, O).
+    //   B (slot 2p+1): block q, tiles [kA, q] on waves [0, w1) -> the other partial of block q;
+    //                  block p, tiles [0, p] on waves [w1, 8) -> final rows of block p.
+    //   solo (odd nqb, last slot): the middle block, all its tiles.
+    // A and B exchange their partials of block q through the scratch buffer (see the epilogue).
+    // Each wave runs over the key tiles tfirst + sin + g*k of its group (g waves); without the
+    // split this is tile s + NS*k of the workgroup's block, as before.
+    int xs_role = 2, xs_pair = 0, xs_q = 0, xs_p = 0, xs_w1 = NS;
+    int qblk = qb, tfirst = 0, tsin = s, tg = NS, ntile = 0;
+    if constexpr (XS) {
+        const int nq = (int)nqb, np = nq >> 1, kA = (nq + 1) >> 1;
+        const int slot = (int)qb_rev;
+        if (slot < 2 * np) {
+            xs_role = slot & 1;
+            xs_pair = slot >> 1;
+            xs_p = xs_pair;
+            xs_q = nq - 1 - xs_pair;
+            if (xs_role == 0) {
+                qblk = xs_q;
+                ntile = kA;
+            } else {
+                const int n1 = xs_q + 1 - kA, n2 = xs_p + 1;
+                int best = 1 << 30;  // waves for block q's tail: least tiles on the busiest wave
+                for (int w1 = 1; w1 < NS; ++w1) {
+                    const int t = max((n1 + w1 - 1) / w1, (n2 + NS - w1 - 1) / (NS - w1));
+                    if (t < best) {
+                        best = t;
+                        xs_w1 = w1;
+                    }
+                }
+                if (s < xs_w1) {
+                    qblk = xs_q;
+                    tfirst = kA;
+                    tg = xs_w1;
+                    ntile = n1;
+                } else {
+                    qblk = xs_p;
+                    tsin = s - xs_w1;
+                    tg = NS - xs_w1;
+                    ntile = n2;
+                }
+            }
+        } else {
+            qblk = np;  // the middle block of an odd count
+            ntile = np + 1;
+        }
+    }
+    const int q0 = qblk * C::BM;
     const int qw0 = q0 + 32 * qg;
     const int qrow = qw0 + c;
     const int qw_last = min(qw0 + 31, S - 1);
@@ -665,7 +741,18 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // into an LDS tile (1 KB per wave-instruction, same swizzle as K) and read by every wave after
     // one barrier, instead of each wave fetching its group's rows from L2.
     half8 qf[D / 16];
-    if constexpr (C::QLDS) {
+    if constexpr (XS) {
+        // Waves 0-3 stage block q's (or the solo block's) 32 rows, waves 4-7 block p's (B only).
+        static_assert(C::QLOADS == 4, "one 32-row Q tile is four wave-instructions");
+        const int qb_tile = (w < 4 || xs_role != 1) ? (xs_role == 1 ? xs_q : qblk) : xs_p;
+        if (w < 4 || xs_role == 1) {
+            const __amdgpu_buffer_rsrc_t qrr = make_rsrc(a.q + (size_t)head * a.q_stride, qspan);
+            const int p = (w & 3) * 64 + lane;
+            const int r = p / C::CH, sl = p % C::CH;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(qrr, (NC_LDS(void) *)(smem + (w < 4 ? C::Q_OFF : XS_Q2) + (w & 3) * 1024),
+                                                     16, (uint32_t)(qb_tile * 32 + r) * qrb + (sl ^ SW::f(r)) * 16, 0, 0, 0);
+        }
+    } else if constexpr (C::QLDS) {
         if (w < C::QLOADS) {
             const __amdgpu_buffer_rsrc_t qrr = make_rsrc(a.q + (size_t)head * a.q_stride, qspan);
             const int p = w * 64 + lane;
@@ -684,10 +771,14 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     constexpr bool PRIV = (NQ == 1);
     const int kv_end = CAUSAL ? min(S, q0 + C::BM) : S;
     int nblk = (kv_end + C::BN - 1) / C::BN;
-    if constexpr (PRIV) {
+    if constexpr (XS) {
+        nblk = tsin < ntile ? (ntile - tsin + tg - 1) / tg : 0;
+    } else if constexpr (PRIV) {
         const int last_key = (CAUSAL ? min(S - 1, qw_last) : S - 1) - C::WK * s;
         nblk = last_key < 0 ? 0 : last_key / C::BN + 1;
     }
+    // First key of the wave's slice in step blk (private staging): key tile tfirst + tsin + tg*blk.
+    auto wave_key0 = [&](int blk) { return 32 * (tfirst + tsin + tg * blk); };
 
     // Staging: wave-instruction t of a block fills 16-byte slots [64t, 64t+64) of the K tile
     // (t < LOADS/2) or of the V tile; the ring stage is a compile-time constant.
@@ -705,7 +796,8 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             const int p = tt * 64 + lane;
             const int r = p / C::CH, sl = p % C::CH;
             const int ch = sl ^ SW::f(r);
-            const uint32_t key = (uint32_t)(blk * C::BN + r);
+            // private staging: row r of the stage is row r - 32s of the wave's 32-key slice
+            const uint32_t key = PRIV ? (uint32_t)(wave_key0(blk) + r - C::WK * s) : (uint32_t)(blk * C::BN + r);
             NC_LDS(void) *dst = (NC_LDS(void) *)(sbase + (isv ? C::TILE : 0) + tt * 1024);
             if (isv)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, key * vrb + ch * 16, 0, 0, 0);
@@ -901,7 +993,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         // The wave's keys in the block are SUB consecutive 32-key sub-tiles, each taken through S^T,
         // softmax and PV before the next (one sub-tile's operands live at a time), so a block of
         // 32*NS*SUB keys costs one wait and one barrier.
-        const int kb = blk * C::BN + C::WK * s;  // the wave's first key in the block
+        const int kb = PRIV ? wave_key0(blk) : blk * C::BN + C::WK * s;  // the wave's first key in the block
         bool run = kb < S;
         if (CAUSAL) run = run && kb <= qw_last;
         if (!run) return;
@@ -921,9 +1013,10 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     with_clamped<0, (NSTAGE > 1 ? NSTAGE - 1 : 1)>(nblk, [&](auto ac) { wait_vm_only<decltype(ac)::value * C::LPW>(); });
     if constexpr (C::QLDS) {
         asm volatile("s_barrier" ::: "memory");  // every wave's part of the Q tile has landed
+        const uint32_t qt = lds0 + ((XS && xs_role == 1 && s >= xs_w1) ? XS_Q2 : C::Q_OFF);
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk)
-            qf[kk] = *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(lds0 + C::Q_OFF + SW::slot(32 * qg + c, 2 * kk + hh) * 16));
+            qf[kk] = *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(qt + SW::slot(32 * qg + c, 2 * kk + hh) * 16));
     }
     tie_regs(qf);
     if (neg_q) {
@@ -963,6 +1056,99 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 const int d = 32 * mt + 8 * i + 4 * hh;
                 if (d < D) *part(s, c, d >> 2) = floatx4{o[mt][4 * i], o[mt][4 * i + 1], o[mt][4 * i + 2], o[mt][4 * i + 3]};
             }
+        if constexpr (XS) {
+            // Pair exchange. Scratch: one u32 counter per pair in a fixed NC_XS_COUNTER_BYTES region,
+            // then per pair two slots (A's, B's): 32 x D f32 unnormalised O, then 32 (m, l) pairs.
+            // Each workgroup of a pair adds 1 to the counter once per launch, so it is even when a
+            // launch starts and odd once one of the two has published its partial. The workgroup
+            // that finds it odd merges both partials into O; the other only publishes. Nothing
+            // waits on the other workgroup, and the counter needs no reset.
+            // Before its barrier, one thread reads the counter: if the partner has already
+            // published, this workgroup merges at once (one round trip for the partner's partial)
+            // and adds its 1 without waiting for the result. Otherwise it publishes its partial,
+            // waits for the stores, adds 1 and merges if the result shows the partner got there in
+            // between.
+            static_assert(C::NT == 512 && DC == 16 && C::BM == 32, "one thread per (row, 4 columns) of a block");
+            constexpr int SLOT = 32 * D * 4 + 32 * 8;
+            uint32_t *xw = reinterpret_cast<uint32_t *>(smem + XS_WORDS);
+            const uint32_t np = nqb >> 1;
+            const size_t pg = (size_t)head * np + (uint32_t)xs_pair;
+            uint32_t *cnt = reinterpret_cast<uint32_t *>(a.scratch) + pg;
+            char *slots = reinterpret_cast<char *>(a.scratch) + NC_XS_COUNTER_BYTES;
+            if (xs_role < 2 && tid == 0) xw[0] = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wait_vm_barrier<0>();
+            const int qi = tid >> 4, ch = tid & 15;
+            // (M, L, O) of row qi, columns 4ch..4ch+3, merged over the waves of group 1 (waves
+            // [0, w1): block q, or the whole workgroup) and of group 2 (B's waves [w1, 8): block p).
+            // Every wave's partial is read once, unconditionally, and split between the groups by
+            // selects (branches here serialised the LDS reads).
+            const int w1 = xs_role == 1 ? xs_w1 : NS;
+            float2v ml[NS];
+            floatx4 pj[NS];
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                ml[j] = mlb[qi * NS + j];
+                pj[j] = *part(j, qi, ch);
+            }
+            float M1 = neg_inf(), M2 = neg_inf();
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                if (j < w1)
+                    M1 = fmaxf(M1, ml[j][0]);
+                else
+                    M2 = fmaxf(M2, ml[j][0]);
+            }
+            float L1 = 0.f, L2 = 0.f;
+            floatx4 o1 = {0.f, 0.f, 0.f, 0.f}, o2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                const bool g1 = j < w1;
+                const float wj = __builtin_amdgcn_exp2f(ml[j][0] - (g1 ? M1 : M2));  // 0 for a wave without keys
+                const float a1 = g1 ? wj : 0.f, a2 = g1 ? 0.f : wj;
+                L1 = __builtin_fmaf(a1, ml[j][1], L1);
+                L2 = __builtin_fmaf(a2, ml[j][1], L2);
+                o1 += a1 * pj[j];
+                o2 += a2 * pj[j];
+            }
+            if (xs_role == 1) {  // block p is B's alone: final rows
+                const int rowp = 32 * xs_p + qi;
+                if (rowp < S) store_o(reinterpret_cast<floatx4 *>(obase + (size_t)rowp * ors + 4 * ch), o2 * __builtin_amdgcn_rcpf(L2));
+            }
+            const int row = 32 * (xs_role == 2 ? qblk : xs_q) + qi;
+            if (xs_role == 2) {
+                if (row < S) store_o(reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch), o1 * __builtin_amdgcn_rcpf(L1));
+                return;
+            }
+            float *mine = reinterpret_cast<float *>(slots + (2 * pg + xs_role) * SLOT);
+            const float *other = reinterpret_cast<const float *>(slots + (2 * pg + (xs_role ^ 1)) * SLOT);
+            bool merge = (xw[0] & 1u) != 0;
+            if (merge) {
+                if (tid == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                store_agent(mine + qi * D + 4 * ch, o1);
+                if (ch == 0) store_agent(mine + 32 * D + 2 * qi, float2v{M1, L1});
+                wait_vm_barrier<0>();  // every wave's part of the partial is stored
+                if (tid == 0) xw[1] = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                wait_vm_barrier<0>();
+                merge = (xw[1] & 1u) != 0;
+            }
+            if (merge) {
+                floatx4 op;
+                float2v mp;
+                load_agent(other + qi * D + 4 * ch, other + 32 * D + 2 * qi, op, mp);
+                // Combined in the fixed order (A's partial, B's partial) whichever workgroup merges,
+                // so the result does not depend on which one arrived last.
+                const bool am_a = xs_role == 0;
+                const floatx4 oa = am_a ? o1 : op, ob = am_a ? op : o1;
+                const float ma = am_a ? M1 : mp[0], mb = am_a ? mp[0] : M1;
+                const float la = am_a ? L1 : mp[1], lb = am_a ? mp[1] : L1;
+                const float mx = fmaxf(ma, mb);
+                const float wa = __builtin_amdgcn_exp2f(ma - mx), wb = __builtin_amdgcn_exp2f(mb - mx);
+                const floatx4 res = (wa * oa + wb * ob) * __builtin_amdgcn_rcpf(__builtin_fmaf(wa, la, wb * lb));
+                if (row < S) store_o(reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch), res);
+            }
+            return;
+        }
         wait_vm_barrier<0>();
         for (int u = tid; u < C::BM * DC; u += C::NT) {
             const int qi = u / DC, ch = u % DC;
@@ -1274,6 +1460,15 @@ NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_full, 64, 2, 4, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q2s4p2_causal, 64, 2, 4, true, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_full, 64, 1, 8, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_causal, 64, 1, 8, true, 2, 1)
+// Pair split (x): causal query blocks p and nqb-1-p shared by two workgroups that exchange partials.
+#define NC_FLASH_XS_KERNEL(NAME, D)                                                                     \
+    extern "C" __global__ __launch_bounds__(512) void NAME(nc_flash_kernel_args a) {                     \
+        flash_fwd_pipe_body<D, 1, 8, true, 2, 1, false, true>(a);                                       \
+    }                                                                                                   \
+    extern "C" __global__ __launch_bounds__(512) void NAME##_bf16(nc_flash_kernel_args a) {              \
+        flash_fwd_pipe_body<D, 1, 8, true, 2, 1, true, true>(a);                                        \
+    }
+NC_FLASH_XS_KERNEL(nc_flash_fwd_d64_q1s8p2x_causal, 64)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_full, 32, 4, 1, false, 3, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_causal, 32, 4, 1, true, 3, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_full, 32, 2, 4, false, 2, 1)

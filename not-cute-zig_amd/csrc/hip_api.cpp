@@ -30,6 +30,10 @@ struct nc_module_st {
     // so a returned nc_function stays valid without the lock.
     std::mutex lock;
     std::unordered_map<std::string, std::unique_ptr<nc_function_st>> functions;
+    // Scratch of the kernels that need one (the pair-split flash kernels), grown on demand and
+    // zeroed when allocated; their exchange counters rely on starting from zero. Guarded by `lock`.
+    void *workspace = nullptr;
+    size_t workspace_bytes = 0;
 };
 
 extern "C" const unsigned char nc_embedded_code_object[];
@@ -192,9 +196,43 @@ int nc_module_load_embedded(nc_module *out) {
 
 int nc_module_unload(nc_module module) {
     if (!module) return fail(NC_ERROR_INVALID_VALUE, "nc_module_unload: null module");
-    int st = check(hipModuleUnload(module->mod), "hipModuleUnload");
+    int st = NC_SUCCESS;
+    if (module->workspace) st = check(hipFree(module->workspace), "hipFree(workspace)");
+    int st2 = check(hipModuleUnload(module->mod), "hipModuleUnload");
     delete module;
-    return st;
+    return st ? st : st2;
+}
+
+// The module's workspace, at least `bytes` long (used by flash.cpp). A larger one replaces it
+// after the device has finished every launch that may still use the old one; a new workspace is
+// zeroed before it is returned.
+extern "C" int nc_internal_module_workspace(nc_module module, size_t bytes, void **out) {
+    if (!module || !out) return fail(NC_ERROR_INVALID_VALUE, "workspace: null argument");
+    std::lock_guard<std::mutex> guard(module->lock);
+    if (module->workspace_bytes < bytes) {
+        if (module->workspace) {
+            int st = check(hipDeviceSynchronize(), "hipDeviceSynchronize(workspace)");
+            if (st) return st;
+            st = check(hipFree(module->workspace), "hipFree(workspace)");
+            module->workspace = nullptr;
+            module->workspace_bytes = 0;
+            if (st) return st;
+        }
+        void *p = nullptr;
+        int st = check(hipMalloc(&p, bytes), "hipMalloc(workspace)");
+        if (st) return st;
+        // hipMemset may return before it completes and is not ordered with non-blocking streams.
+        st = check(hipMemset(p, 0, bytes), "hipMemset(workspace)");
+        if (!st) st = check(hipDeviceSynchronize(), "hipDeviceSynchronize(workspace)");
+        if (st) {
+            (void)hipFree(p);
+            return st;
+        }
+        module->workspace = p;
+        module->workspace_bytes = bytes;
+    }
+    *out = module->workspace;
+    return NC_SUCCESS;
 }
 
 int nc_module_get_function(nc_function *out, nc_module module, const char *name) {

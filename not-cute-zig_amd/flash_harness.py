@@ -146,7 +146,7 @@ class Device:
         opts = self.wl.options()
         sel = nc.select_kernel(opts)
         fn = module.get_function(sel.name.decode())
-        args = nc.pack_args(opts, sel, *[b.ptr for b in self.bufs])
+        args = nc.pack_args(opts, sel, *[b.ptr for b in self.bufs], module=module)
         return sel, nc.run_kernel(fn, tuple(sel.grid), (sel.threads,), [args], warmup=warmup, iters=iters,
                                   bytes_=bytes_, flops=flops)
 

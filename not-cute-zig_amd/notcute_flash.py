@@ -79,6 +79,7 @@ class KernelSelection(ctypes.Structure):
         ("kv_splits", ctypes.c_uint32),
         ("lds_bytes", ctypes.c_uint32),
         ("aligned", ctypes.c_uint32),
+        ("scratch_bytes", ctypes.c_uint64),
     ]
 
 
@@ -102,8 +103,7 @@ class KernelArgs(ctypes.Structure):
         ("o_row_stride", ctypes.c_uint64),
         ("batch_heads", ctypes.c_uint32),
         ("num_q_blocks", ctypes.c_uint32),
-        ("reserved0", ctypes.c_uint32),
-        ("reserved1", ctypes.c_uint32),
+        ("scratch", ctypes.c_void_p),
     ]
 
 
@@ -236,6 +236,9 @@ _SIGS = {
         [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t,
          ctypes.POINTER(FlashOptions), _P]),
     "nc_flash_work_model": (ctypes.c_int, [ctypes.POINTER(FlashOptions), ctypes.POINTER(FlashWork)]),
+    "nc_flash_reserve_workspace": (ctypes.c_int, [_P, ctypes.POINTER(FlashOptions), ctypes.POINTER(_P)]),
+    "nc_flash_kernel_scratch_bytes": (
+        ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(FlashOptions), ctypes.POINTER(_U64)]),
     "nc_benchmark_options_init": (None, [ctypes.POINTER(BenchmarkOptions)]),
     "nc_benchmark_run_kernel": (
         ctypes.c_int,
@@ -338,11 +341,34 @@ def work_model(opts: FlashOptions) -> FlashWork:
     return w
 
 
-def pack_args(opts: FlashOptions, sel: KernelSelection, q: int, k: int, v: int, o: int) -> KernelArgs:
+def pack_args(opts: FlashOptions, sel: KernelSelection, q: int, k: int, v: int, o: int,
+              module: Optional["Module"] = None) -> KernelArgs:
+    """The kernel argument block for `sel`. A kernel that needs scratch memory (sel.scratch_bytes > 0)
+    gets `module`'s workspace, reserved here; without a module such a selection is refused."""
     a = KernelArgs()
     check(lib().nc_flash_pack_args(ctypes.byref(opts), ctypes.byref(sel), q, k, v, o, ctypes.byref(a)),
           "flash.packArgs")
+    if sel.scratch_bytes:
+        if module is None:
+            raise ValueError(f"{sel.name.decode()} needs {sel.scratch_bytes} bytes of scratch: pass the module")
+        a.scratch = reserve_workspace(module, opts)
     return a
+
+
+def kernel_scratch_bytes(name: str, opts: FlashOptions) -> int:
+    """nc_flash_kernel_scratch_bytes: scratch the named kernel needs for `opts` (0 for most)."""
+    n = ctypes.c_uint64()
+    check(lib().nc_flash_kernel_scratch_bytes(name.encode(), ctypes.byref(opts), ctypes.byref(n)),
+          "flash.kernelScratchBytes")
+    return int(n.value)
+
+
+def reserve_workspace(module: "Module", opts: FlashOptions) -> Optional[int]:
+    """nc_flash_reserve_workspace: the module's workspace sized for `opts` (None when not needed)."""
+    p = ctypes.c_void_p()
+    check(lib().nc_flash_reserve_workspace(module.handle, ctypes.byref(opts), ctypes.byref(p)),
+          "flash.reserveWorkspace")
+    return p.value
 
 
 # ---------------------------------------------------------------------------------------------

@@ -319,3 +319,34 @@ def test_code_object_exports_reference_kernel_symbols():
                  "flash_attention_fwd_h64_bn32", "flash_attention_fwd_h64_causal"):
         assert name.encode() + b"\0" in blob, name
     assert b"\0flash_attention_fwd\0" in blob
+
+
+def test_pair_split_dispatch_region():
+    """The pair-split kernel replaces the private-staging one for d=64 causal shapes with at least 96
+    query blocks whose grid fits one workgroup per CU (measured faster there, slower elsewhere)."""
+    from flash_workloads import Workload
+
+    for bh in (1, 2, 3, 4, 8):
+        for s in (1024, 2048, 3040, 3041, 3072, 4096, 8192, 8193, 16384):
+            for d, causal in ((64, True), (64, False), (32, True)):
+                sel = nc.select_kernel(Workload("x", bh, s, d, causal, 0.1, (("normal", 0, 1),) * 3).options())
+                nqb = (s + 31) // 32
+                q1s8 = "q1s8p2" in sel.name.decode()
+                want = d == 64 and causal and nqb >= 96 and nqb * bh <= 256
+                assert ("q1s8p2x" in sel.name.decode()) == (want and q1s8), (bh, s, d, causal, sel.name)
+                if "q1s8p2x" in sel.name.decode():
+                    pairs = bh * (nqb // 2)
+                    assert sel.scratch_bytes == 65536 + pairs * 2 * (32 * 64 * 4 + 32 * 8)
+                    assert (sel.grid[0], sel.threads, sel.block_m) == (nqb * bh, 512, 32)
+                else:
+                    assert sel.scratch_bytes == 0
+
+
+def test_kernel_scratch_bytes_by_name():
+    o = CONFIGS["c3"].options()
+    assert nc.kernel_scratch_bytes("nc_flash_fwd_d64_q1s8p2x_causal", o) == 65536 + 128 * 2 * 8448
+    assert nc.kernel_scratch_bytes("nc_flash_fwd_d64_q1s8p2x_causal_bf16", o) == 65536 + 128 * 2 * 8448
+    assert nc.kernel_scratch_bytes("nc_flash_fwd_d64_q1s8p2_causal", o) == 0
+    with pytest.raises(nc.NcError) as e:
+        nc.kernel_scratch_bytes("flash_attention_fwd_v2", o)
+    assert e.value.name == "NotFound"
