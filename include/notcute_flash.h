@@ -300,6 +300,18 @@ int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, con
                           size_t k_len, const uint16_t *v, size_t v_len, float *o, size_t o_len,
                           const nc_flash_options *opts, nc_stream stream);
 
+/* No counterpart in the reference (whose kernels use no scratch memory): for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The same launch as nc_flash_launch_async, except that a kernel needing scratch gets a
+ * static device buffer of NC_NOALLOC_SCRATCH_BYTES compiled into this library (one per GPU, held
+ * until the process ends) instead of the module's workspace; it never allocates or frees anything.
+ * NC_ERROR_INVALID_VALUE when the selected kernel would need more scratch than that. Every call on
+ * one GPU shares the buffer: calls that overlap in time on one GPU (e.g. on two streams) race. */
+#define NC_NOALLOC_SCRATCH_BYTES (4u << 20)
+int nc_flash_launch_noalloc(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k,
+                            size_t k_len, const uint16_t *v, size_t v_len, float *o, size_t o_len,
+                            const nc_flash_options *opts, nc_stream stream);
+
 /* Extension (no counterpart in the reference, whose kernels use no scratch memory): make the
  * module's workspace large enough for a launch with these options, allocating it now (device memory,
  * zeroed), so that later launches allocate nothing. Stores the workspace in *workspace (may be NULL)

@@ -308,9 +308,15 @@ int nc_flash_pack_args(const nc_flash_options *opts, const nc_flash_kernel_selec
     return NC_SUCCESS;
 }
 
-int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
-                          const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts,
-                          nc_stream stream) {
+}  // extern "C"
+
+namespace {
+
+// flash.launch for both entry points: the scratch of a kernel that needs one comes from the module's
+// workspace (scratch == nullptr) or from the caller's buffer of scratch_cap bytes.
+int flash_launch_impl(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
+                      const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts,
+                      nc_stream stream, void *scratch, size_t scratch_cap) {
     int st = nc_flash_validate(opts);  // src/flash.zig:39
     if (st) return st;
     if (!module || !q || !k || !v || !o) return NC_ERROR_INVALID_VALUE;
@@ -331,8 +337,13 @@ int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, con
     st = nc_flash_pack_args(opts, &sel, q, k, v, o, &args);
     if (st) return st;
     if (sel.scratch_bytes) {
-        st = nc_internal_module_workspace(module, sel.scratch_bytes, &args.scratch);
-        if (st) return st;
+        if (scratch) {
+            if (sel.scratch_bytes > scratch_cap) return NC_ERROR_INVALID_VALUE;
+            args.scratch = scratch;
+        } else {
+            st = nc_internal_module_workspace(module, sel.scratch_bytes, &args.scratch);
+            if (st) return st;
+        }
     }
     nc_launch_config cfg;
     std::memset(&cfg, 0, sizeof cfg);
@@ -346,6 +357,25 @@ int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, con
     cfg.stream = stream;
     void *params[] = {&args};
     return nc_function_launch(fn, &cfg, params);
+}
+
+}  // namespace
+
+extern "C" {
+
+int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
+                          const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts,
+                          nc_stream stream) {
+    return flash_launch_impl(module, q, q_len, k, k_len, v, v_len, o, o_len, opts, stream, nullptr, 0);
+}
+
+// For noalloc.hip: the same launch with a caller-provided scratch buffer of `cap` bytes (never the
+// module's workspace); NC_ERROR_INVALID_VALUE when the selected kernel needs more than `cap`.
+int nc_internal_flash_launch_scratch(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k,
+                                     size_t k_len, const uint16_t *v, size_t v_len, float *o, size_t o_len,
+                                     const nc_flash_options *opts, nc_stream stream, void *scratch, size_t cap) {
+    if (!scratch) return NC_ERROR_INVALID_VALUE;
+    return flash_launch_impl(module, q, q_len, k, k_len, v, v_len, o, o_len, opts, stream, scratch, cap);
 }
 
 int nc_flash_launch(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,

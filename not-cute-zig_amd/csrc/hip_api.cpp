@@ -88,6 +88,12 @@ int fail(int status, const char *what) {
 
 }  // namespace
 
+// Error helpers for the library's other translation units (flash.cpp, noalloc.hip).
+extern "C" int nc_internal_check(int hip_error, const char *what) { return check((hipError_t)hip_error, what); }
+extern "C" int nc_internal_fail(int status, const char *what) { return fail(status, what); }
+// noalloc.hip: the device address of its static scratch on the current device.
+extern "C" int nc_internal_noalloc_setup(void);
+
 extern "C" {
 
 const char *nc_status_name(int status) {
@@ -122,6 +128,8 @@ int nc_init(void) {
     int st = check(e, "hipGetDeviceCount");
     if (st) return st;
     st = check(hipSetDevice(0), "hipSetDevice(0)");
+    if (st) return st;
+    st = nc_internal_noalloc_setup();  // the static scratch of nc_flash_launch_noalloc on device 0
     if (st) return st;
     g_initialized = true;
     return NC_SUCCESS;

@@ -236,6 +236,10 @@ _SIGS = {
         [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t,
          ctypes.POINTER(FlashOptions), _P]),
     "nc_flash_work_model": (ctypes.c_int, [ctypes.POINTER(FlashOptions), ctypes.POINTER(FlashWork)]),
+    "nc_flash_launch_noalloc": (
+        ctypes.c_int,
+        [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t,
+         ctypes.POINTER(FlashOptions), _P]),
     "nc_flash_reserve_workspace": (ctypes.c_int, [_P, ctypes.POINTER(FlashOptions), ctypes.POINTER(_P)]),
     "nc_flash_kernel_scratch_bytes": (
         ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(FlashOptions), ctypes.POINTER(_U64)]),
