@@ -1245,21 +1245,51 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
 //
 // Workgroup (bx, by): query rows 16bx .. 16bx+15 of slice by. Every wave computes those 16 rows
 // over every NW-th 32-key chunk with 16x16x32 MFMAs in the transposed form (S^T = K Q^T,
-// O^T += V^T P^T); operands are gathered element by element from global memory (no alignment
-// assumed), the softmax takes each chunk's max after scaling (any sign of scale), and the waves'
-// partials merge through LDS. Lane l holds query l%16; in S^T tile t it holds keys 16t+4(l/16)+r,
+// O^T += V^T P^T); with 16-byte aligned slices each wave stages its chunks of K and V through its
+// own LDS region, otherwise operands are gathered element by element from global memory (no
+// alignment assumed); the softmax takes each chunk's max after scaling (any sign of scale), and the
+// waves' partials merge through LDS. Lane l holds query l%16; in S^T tile t it holds keys 16t+4(l/16)+r,
 // and those 8 keys are, in order, its k-values of the P^T and V^T operands.
 // ---------------------------------------------------------------------------------------------
 constexpr int kRefMaxWaves = 4;
 
+// LDS of the reference-ABI body: per wave, one staged 32-key chunk of K and of V (rows padded to
+// D + 8 halves: the K reads of 16 rows at one column chunk and the transposed V reads then spread
+// over the banks), reused after the key loop for the waves' merge.
 template <int D>
+struct RefCfg {
+    static constexpr int KP = D + 8;                 // staged row pitch, halves
+    static constexpr int CHUNK = 32 * KP * 2;        // bytes of one staged K (or V) chunk
+    static constexpr int WAVE = 2 * CHUNK;
+    static constexpr int OP = D + 4;                 // merge row pitch, floats
+    static constexpr int MERGE = kRefMaxWaves * 16 * (8 + OP * 4);
+    static constexpr int LDS = kRefMaxWaves * WAVE > MERGE ? kRefMaxWaves * WAVE : MERGE;
+    static constexpr int SEG = 32 * (D / 8) / 64;    // 16-byte segments of a chunk per lane
+};
+constexpr int kRefLds = RefCfg<64>::LDS;
+
+template <int N>
+__device__ __forceinline__ void wait_lds_tied_any(u32x2 (&v)[N]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+
+// VEC: every Q/K/V slice base is 16-byte aligned (pointers and slice strides; rows of D halves
+// are), so each wave loads a key chunk as one contiguous run of 16-byte segments, stages it in its
+// own LDS region (the next chunk's loads in flight meanwhile) and reads the MFMA operands there:
+// K rows by ds_read_b128, V^T by ds_read_b64_tr_b16 (lane m of a 16-lane group supplies
+// V[r0 + m/4][d0 + 4(m%4)], lane i receives V[r0..r0+3][d0 + i]). Otherwise every operand element
+// is gathered from global memory (any stride, any base alignment).
+template <int D, bool VEC>
 __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                                                       float *o, int S, uint64_t q_stride, uint64_t k_stride,
                                                       uint64_t v_stride, uint64_t o_stride, float scale,
                                                       bool causal, char *smem) {
+    using RC = RefCfg<D>;
     constexpr int DH = (D + 31) / 32;  // 32-column k-steps of S^T
     constexpr int DT = D / 16;         // 16-row O^T tiles
-    constexpr int OP = D + 4;
+    constexpr int OP = RC::OP;
     const int NW = (int)(blockDim.x >> 6);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
@@ -1282,9 +1312,41 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
         }
         return x;
     };
+    auto load8 = [&](const uint16_t *base, int row, int d0) {  // the same by one 16-byte load
+        u32x4 t = {0u, 0u, 0u, 0u};
+        if (row < S && d0 < D) t = *reinterpret_cast<const u32x4 *>(base + (size_t)row * D + d0);
+        return __builtin_bit_cast(half8, t);
+    };
     half8 qf[DH];
 #pragma unroll
-    for (int h = 0; h < DH; ++h) qf[h] = gather8(qh, qrow, 32 * h + 8 * g);
+    for (int h = 0; h < DH; ++h) qf[h] = VEC ? load8(qh, qrow, 32 * h + 8 * g) : gather8(qh, qrow, 32 * h + 8 * g);
+
+    // This wave's staging region (VEC): K rows at kst, V rows at kst + CHUNK, pitch KP halves.
+    // This wave's staging region (VEC): K rows at kst, V rows at kst + CHUNK, pitch KP halves; the
+    // next chunk's rows travel in registers while the current one is computed (deeper register
+    // prefetch measured no faster).
+    const uint32_t kst = (uint32_t)(uintptr_t)smem + w * RC::WAVE;
+    const uint32_t vst = kst + RC::CHUNK;
+    u32x4 kreg[RC::SEG > 0 ? RC::SEG : 1], vreg[RC::SEG > 0 ? RC::SEG : 1];
+    auto fetch = [&](int ch) {  // chunk ch's K and V rows into registers, zero past seq_len
+#pragma unroll
+        for (int j = 0; j < RC::SEG; ++j) {
+            const int seg = lane + 64 * j, row = seg / (D / 8), c8 = seg % (D / 8), key = 32 * ch + row;
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            kreg[j] = key < S ? *reinterpret_cast<const u32x4 *>(kh + (size_t)key * D + 8 * c8) : z;
+            vreg[j] = key < S ? *reinterpret_cast<const u32x4 *>(vh + (size_t)key * D + 8 * c8) : z;
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int j = 0; j < RC::SEG; ++j) {
+            const int seg = lane + 64 * j, row = seg / (D / 8), c8 = seg % (D / 8);
+            const uint32_t off = (uint32_t)(row * RC::KP + 8 * c8) * 2;
+            *reinterpret_cast<NC_LDS(u32x4) *>((uintptr_t)(kst + off)) = kreg[j];
+            *reinterpret_cast<NC_LDS(u32x4) *>((uintptr_t)(vst + off)) = vreg[j];
+        }
+    };
+    if (VEC && w < nch) fetch(w);
 
     const float sc = scale * kLog2e;
     float mrow = neg_inf(), l = 0.f;
@@ -1295,13 +1357,40 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
 
     for (int ch = w; ch < nch; ch += NW) {
         const int kt0 = 32 * ch;
+        if constexpr (VEC) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous chunk's reads are done
+            stage();
+            asm volatile("" ::: "memory");
+            if (ch + NW < nch) fetch(ch + NW);  // in flight while this chunk is computed
+        }
         floatx4 s[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             s[t] = floatx4{};
 #pragma unroll
-            for (int h = 0; h < DH; ++h)
-                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(gather8(kh, kt0 + 16 * t + c, 32 * h + 8 * g), qf[h], s[t], 0, 0, 0);
+            for (int h = 0; h < DH; ++h) {
+                half8 kf;
+                if constexpr (VEC) {
+                    const int d0 = 32 * h + 8 * g;
+                    kf = half8{};
+                    if (d0 < D)
+                        kf = *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(kst + (uint32_t)((16 * t + c) * RC::KP + d0) * 2));
+                } else {
+                    kf = gather8(kh, kt0 + 16 * t + c, 32 * h + 8 * g);
+                }
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[h], s[t], 0, 0, 0);
+            }
+        }
+        // V^T operands (VEC): issued now, their latency hidden behind the softmax.
+        u32x2 vt[VEC ? 2 * DT : 1];
+        if constexpr (VEC) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int r = 16 * hf + 4 * g + (c >> 2), d0 = 16 * dt + 4 * (c & 3);
+                    ds_read_tr<0>(vt[2 * dt + hf], vst + (uint32_t)(r * RC::KP + d0) * 2);
+                }
         }
         float x[8];
         float lm = neg_inf();
@@ -1328,23 +1417,32 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
             const half2v hp = {pb[2 * t], pb[2 * t + 1]};
             l = __builtin_amdgcn_fdot2(hp, ones, l, false);
         }
+        if constexpr (VEC) wait_lds_tied_any(vt);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-            half8 va = {};
-            const int d = 16 * dt + c;
+            half8 va;
+            if constexpr (VEC) {
+                const u32x4 vv = {vt[2 * dt][0], vt[2 * dt][1], vt[2 * dt + 1][0], vt[2 * dt + 1][1]};
+                va = __builtin_bit_cast(half8, vv);
+            } else {
+                va = half8{};
+                const int d = 16 * dt + c;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int key = kt0 + 16 * (e >> 2) + 4 * g + (e & 3);
-                if (key < S) va[e] = __builtin_bit_cast(_Float16, vh[(size_t)key * D + d]);
+                for (int e = 0; e < 8; ++e) {
+                    const int key = kt0 + 16 * (e >> 2) + 4 * g + (e & 3);
+                    if (key < S) va[e] = __builtin_bit_cast(_Float16, vh[(size_t)key * D + d]);
+                }
             }
             oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, oacc[dt], 0, 0, 0);
         }
     }
 
-    // Merge the waves' partials: per-query (m, l) and scaled O^T through LDS.
+    // Merge the waves' partials: per-query (m, l) and scaled O^T through LDS (over the staging
+    // regions, once every wave is past its loop).
     float lt = l + __shfl_xor(l, 16);
     lt += __shfl_xor(lt, 32);
-    float2v *mlb = reinterpret_cast<float2v *>(smem);                              // [NW][16]
+    __syncthreads();
+    float2v *mlb = reinterpret_cast<float2v *>(smem);                                  // [NW][16]
     float *ob = reinterpret_cast<float *>(smem + kRefMaxWaves * 16 * sizeof(float2v));  // [NW][16][OP]
     if (g == 0) mlb[w * 16 + c] = float2v{mrow, lt};
     __syncthreads();
@@ -1378,19 +1476,27 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
                                                  uint64_t seq_len, uint64_t head_dim, uint64_t q_stride,
                                                  uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, float scale,
                                                  uint32_t causal) {
-    __shared__ __attribute__((aligned(16))) char smem[kRefMaxWaves * 16 * (8 + (64 + 4) * 4)];
+    __shared__ __attribute__((aligned(16))) char smem[kRefLds];
     // Shapes the reference's kernels reject return without writing (src/flash_h64_bn32.zig:40).
     if (seq_len == 0 || seq_len > 0x7fffffffull || (blockDim.x & 63) || blockDim.x > 64 * kRefMaxWaves) return;
     const int S = (int)seq_len;
     const bool cz = ALWAYS_CAUSAL || causal != 0;
-    if (head_dim == 64)
-        flash_fwd_refabi_body<64>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, cz, smem);
-    else if (D64_ONLY)
+    // 16-byte vector path when every slice base is 16-byte aligned (rows of head_dim halves are).
+    const bool vec = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                       reinterpret_cast<uintptr_t>(v)) & 15u) == 0 && ((q_stride | k_stride | v_stride) & 7u) == 0;
+    auto run = [&](auto dc, auto vc) {
+        flash_fwd_refabi_body<decltype(dc)::value, decltype(vc)::value != 0>(q, k, v, o, S, q_stride, k_stride, v_stride,
+                                                                              o_stride, scale, cz, smem);
+    };
+    if (head_dim == 64) {
+        if (vec) run(IC<64>{}, IC<1>{}); else run(IC<64>{}, IC<0>{});
+    } else if (D64_ONLY) {
         return;
-    else if (head_dim == 16)
-        flash_fwd_refabi_body<16>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, cz, smem);
-    else if (head_dim == 32)
-        flash_fwd_refabi_body<32>(q, k, v, o, S, q_stride, k_stride, v_stride, o_stride, scale, cz, smem);
+    } else if (head_dim == 16) {
+        if (vec) run(IC<16>{}, IC<1>{}); else run(IC<16>{}, IC<0>{});
+    } else if (head_dim == 32) {
+        if (vec) run(IC<32>{}, IC<1>{}); else run(IC<32>{}, IC<0>{});
+    }
 }
 
 }  // namespace
