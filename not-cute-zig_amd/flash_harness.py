@@ -8,6 +8,8 @@ runner (modal_run.py:34-69), on one MI355X through the C ABI.
     python flash_harness.py baselines             # PyTorch SDPA on the same shapes (tools/pytorch_baselines.py)
     python flash_harness.py materialized          # rocBLAS QK^T -> softmax -> PV (tools/cuda_baselines.cu:689-759)
     python flash_harness.py profile-flash         # runProfileFlash (src/main.zig:81-130)
+    python flash_harness.py profile-flash --counters DIR   # the same under rocprofv3 counter passes
+                                                  # (the Nsight Compute run of modal_run.py:108-146)
     python flash_harness.py benchmark-flash       # runFlashBenchmark (src/main.zig:760-766)
     python flash_harness.py compare-table FILE... # the baseline-vs-not-cute table (modal_run.py:34-69)
 
@@ -21,9 +23,13 @@ used only for its host-side input fills.
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import math
 import os
+import shutil
+import subprocess
 import sys
 from typing import Dict, Iterable, List, Optional, Sequence, Tuple
 
@@ -412,6 +418,102 @@ def cmd_profile(module: nc.Module, args) -> int:
     return _compare_one(module, wl, args)
 
 
+# Counter passes of `profile-flash --counters`, the MI355X counterpart of the reference's Nsight
+# Compute run (modal_run.py:108-146: speedOfLight, Occupancy, SchedulerStats, WarpStateStats and
+# MemoryWorkloadAnalysis sections). rocprofv3 does not split counters over passes, so each pass is
+# its own profiler run holding at most 8 SQ, 4 TCC (FETCH_SIZE takes 3, WRITE_SIZE 2) and 2 GRBM
+# counters.
+COUNTER_PASSES = [
+    ("trace", ["--kernel-trace", "--stats"]),
+    ("speed_of_light", ["--pmc", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F16",
+                        "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_ACTIVE_INST_VALU", "SQ_INSTS_VALU", "SQ_INSTS_MFMA",
+                        "GRBM_GUI_ACTIVE"]),
+    ("scheduler", ["--pmc", "SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_ANY",
+                   "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_WAIT_INST_LDS"]),
+    ("lds", ["--pmc", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_ADDR_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_ACTIVE_INST_LDS"]),
+    ("hbm_read", ["--pmc", "FETCH_SIZE"]),
+    ("hbm_write", ["--pmc", "WRITE_SIZE"]),
+    ("l2", ["--pmc", "TCC_HIT_sum", "TCC_MISS_sum"]),
+]
+SIMDS = 1024  # 256 CUs x 4 SIMDs
+XCDS = 8      # GRBM_GUI_ACTIVE is reported summed over the XCDs
+
+
+def _read_counters(outdir: str, kernel: str) -> Tuple[Dict[str, float], int]:
+    """Per-dispatch means of every counter of `kernel` in a pass's counter_collection CSV files."""
+    vals: Dict[str, List[float]] = {}
+    for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Kernel_Name", "").split("(")[0].strip() == kernel:
+                    vals.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    n = max((len(v) for v in vals.values()), default=0)
+    return {k: sum(v) / len(v) for k, v in vals.items()}, n
+
+
+def _read_trace(outdir: str, kernel: str) -> Dict[str, float]:
+    for path in glob.glob(os.path.join(outdir, "**", "*kernel_stats.csv"), recursive=True):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row["Name"].split("(")[0].strip() == kernel:
+                    return {"calls": int(row["Calls"]), "average_ns": float(row["AverageNs"]),
+                            "min_ns": float(row["MinNs"]), "max_ns": float(row["MaxNs"])}
+    return {}
+
+
+def cmd_profile_counters(args) -> int:
+    """Run `profile-flash` once per counter pass under rocprofv3 (each pass a child process of its
+    own, started before this process touches the GPU) and summarise the selected kernel's counters
+    per dispatch."""
+    rocprof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    kernel = nc.select_kernel(nc.options(batch_heads=8, seq_len=1024, head_dim=64, scale=0.125,
+                                         causal=True)).name.decode()
+    outroot = os.path.abspath(args.counters)
+    env = dict(os.environ, TMPDIR="/tmp")
+    child = [sys.executable, os.path.abspath(__file__), "profile-flash", "--warmup", str(args.warmup),
+             "--iters", str(args.iters)]
+    res: Dict[str, Dict] = {}
+    for name, extra in COUNTER_PASSES:
+        outdir = os.path.join(outroot, name)
+        cmd = [rocprof, *extra, "-f", "csv", "-d", outdir, "-o", name, "--", *child]
+        log(f"profile: pass {name}: {' '.join(cmd)}")
+        try:
+            p = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True, timeout=args.pass_timeout)
+        except subprocess.TimeoutExpired:
+            log(f"profile: pass {name} timed out after {args.pass_timeout} s")
+            return 1
+        # rocprofv3 may end with a segmentation fault after the program has finished and its files
+        # are complete; the files decide.
+        res[name] = _read_trace(outdir, kernel) if name == "trace" else dict(zip(("counters", "dispatches"),
+                                                                                 _read_counters(outdir, kernel)))
+        if not res[name] or (name != "trace" and not res[name]["dispatches"]):
+            log(f"profile: pass {name} produced no record of {kernel} (rc {p.returncode}): {p.stderr[-400:]}")
+            return 1
+    c = {k: v for name, _ in COUNTER_PASSES[1:] for k, v in res[name]["counters"].items()}
+    gui = c["GRBM_GUI_ACTIVE"] / XCDS  # GPU-busy cycles of one XCD during the dispatch
+    summary = {
+        "kernel": kernel, "dispatches": res["speed_of_light"]["dispatches"],
+        "duration_us": res["trace"]["average_ns"] / 1e3,
+        "grbm_gui_active_per_xcd": gui,
+        "mfma_busy_pct": 100.0 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * SIMDS),
+        "mfma_flops": c["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512,
+        "valu_mfma_coexec_pct_of_mfma": 100.0 * c["SQ_VALU_MFMA_COEXEC_CYCLES"] / max(c["SQ_VALU_MFMA_BUSY_CYCLES"], 1.0),
+        "waves": c["SQ_WAVES"], "wait_any_pct_of_wave_cycles": 100.0 * c["SQ_WAIT_ANY"] / max(c["SQ_WAVE_CYCLES"], 1.0),
+        "insts_per_wave": {k: c[k] / max(c["SQ_WAVES"], 1.0) for k in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_SALU",
+                                                                      "SQ_INSTS_LDS")},
+        "lds_bank_conflict_cycles": c["SQ_LDS_BANK_CONFLICT"],
+        "fetch_kib": c["FETCH_SIZE"], "write_kib": c["WRITE_SIZE"],
+        "l2_hit_pct": 100.0 * c["TCC_HIT_sum"] / max(c["TCC_HIT_sum"] + c["TCC_MISS_sum"], 1.0),
+        "counters": c,
+    }
+    log(f"profile: {kernel}: {summary['duration_us']:.2f} us per dispatch, MFMA busy {summary['mfma_busy_pct']:.1f} % "
+        f"of SIMD cycles, VALU co-issued with {summary['valu_mfma_coexec_pct_of_mfma']:.1f} % of MFMA cycles, "
+        f"waves waiting {summary['wait_any_pct_of_wave_cycles']:.1f} % of their cycles, L2 hit {summary['l2_hit_pct']:.1f} %, "
+        f"FETCH_SIZE {summary['fetch_kib']:.1f} KiB, WRITE_SIZE {summary['write_kib']:.1f} KiB")
+    print(json.dumps({"profile_counters": summary}, separators=(",", ":")), flush=True)
+    return 0
+
+
 def _compare_one(module: nc.Module, wl: Workload, args) -> int:
     shape = shape_name(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
     flops, bytes_ = reference_work(wl.batch_heads, wl.seq_len, wl.head_dim, wl.causal)
@@ -520,6 +622,10 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
               sub.add_parser("benchmark-flash", help="runFlashBenchmark's five cases")):
         q.add_argument("--warmup", type=int, default=5)
         q.add_argument("--iters", type=int, default=20)
+    pf = sub.choices["profile-flash"]
+    pf.add_argument("--counters", metavar="DIR", default="",
+                    help="run under rocprofv3 counter passes, writing them under DIR, and summarise")
+    pf.add_argument("--pass-timeout", type=float, default=120.0, help="seconds per profiler pass")
     t = sub.add_parser("compare-table", help="print the baseline table from JSONL files ('-' = stdin)")
     t.add_argument("files", nargs="+")
     args = ap.parse_args(argv)
@@ -527,6 +633,8 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
         return cmd_table(args)
     if args.cmd == "baselines":
         return cmd_baselines(args)
+    if args.cmd == "profile-flash" and args.counters:
+        return cmd_profile_counters(args)  # before any GPU call: the passes are child processes
     nc.init()
     module = nc.Module.load_embedded()
     return {"flash": cmd_flash, "compare": cmd_compare, "profile-flash": cmd_profile,

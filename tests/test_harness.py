@@ -87,3 +87,21 @@ def test_benchmark_fills():
     assert q.tolist() == [((3 * i + 1) % 11) * 0.125 for i in range(12)]
     v = fh.modular_fill(20, 7, 3, 17, 0.03125).view(np.float16).astype(np.float32)
     assert v.tolist() == [((7 * i + 3) % 17) * 0.03125 for i in range(20)]
+
+
+def test_profile_counter_passes_fit_the_hardware():
+    """Each rocprofv3 pass of `profile-flash --counters` stays within one pass's counter budget (at
+    most 8 SQ, 4 TCC with FETCH_SIZE taking 3 and WRITE_SIZE 2, 2 GRBM) and never combines --pmc
+    with a trace option."""
+    import flash_harness as fh
+
+    tcc_cost = {"FETCH_SIZE": 3, "WRITE_SIZE": 2, "TCC_HIT_sum": 1, "TCC_MISS_sum": 1}
+    for name, args in fh.COUNTER_PASSES:
+        if "--pmc" not in args:
+            assert args == ["--kernel-trace", "--stats"], name
+            continue
+        assert not any(a.startswith("-") and a != "--pmc" for a in args), name
+        ctrs = [a for a in args if a != "--pmc"]
+        assert sum(c.startswith("SQ_") for c in ctrs) <= 8, name
+        assert sum(c.startswith("GRBM_") for c in ctrs) <= 2, name
+        assert sum(tcc_cost.get(c, 1) for c in ctrs if c.startswith(("TCC_", "FETCH", "WRITE"))) <= 4, name
