@@ -5,10 +5,9 @@ previous tile's: each stays far below f16's 65504, but a lane's 16 weights sum p
 third tile only 8 keys take the new level (the rest stay at the previous one), so lane sums stay
 under 65504 and weights of ~5000 are carried into f16 unscaled; the tile after that is two levels
 up, where single weights overflow f16.
-- Kernels that add the f32 weights for the row sum must take a lane sum of 65504 or more as the
-  sign to move the max (a weight that rounds to infinity is >= 65520).
-- Kernels that add the rounded weights move it only on an infinite sum.
-Every path must match the oracle.
+The f16 kernels add the rounded weights, so a weight that overflowed makes the lane sum infinite
+and only that moves the max; the bf16 kernels move it once a lane sum reaches 2^20. Every path must
+match the oracle.
 
 The large-|V| cases pin the row sum itself. The lazy max leaves weights of up to 65504 in P, each
 rounded to f16 for the PV product; a kernel that divided by the sum of the *unrounded* weights
