@@ -350,3 +350,65 @@ def test_kernel_scratch_bytes_by_name():
     with pytest.raises(nc.NcError) as e:
         nc.kernel_scratch_bytes("flash_attention_fwd_v2", o)
     assert e.value.name == "NotFound"
+
+
+# C struct name of each ctypes mirror. A foreign binding (the Zig `@cImport` of the header that
+# INTEGRATION.md sketches, ctypes here) maps its fields onto exactly these offsets and sizes.
+_ABI_STRUCTS = {
+    "nc_flash_options": nc.FlashOptions,
+    "nc_flash_kernel_selection": nc.KernelSelection,
+    "nc_flash_kernel_args": nc.KernelArgs,
+    "nc_launch_config": nc.LaunchConfig,
+    "nc_function_attributes": nc.FunctionAttributes,
+    "nc_device_attributes": nc.DeviceAttributes,
+    "nc_flash_work": nc.FlashWork,
+    "nc_benchmark_options": nc.BenchmarkOptions,
+    "nc_benchmark_result": nc.BenchmarkResult,
+}
+
+
+def test_header_struct_layout_matches_binding(tmp_path):
+    """Every struct of include/notcute_flash.h, compiled by gcc, has the field names, offsets and
+    sizes (and the total size) of the binding's mirror, so a binding generated from the header
+    (Zig's @cImport) and the ctypes one agree on the ABI."""
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "notcute_flash.h"', "int main(void) {"]
+    for cname, py in _ABI_STRUCTS.items():
+        lines.append(f'printf("{cname} - %zu %zu\\n", sizeof({cname}), _Alignof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'printf("{cname} {fname} %zu %zu\\n", offsetof({cname}, {fname}), '
+                         f'sizeof((({cname} *)0)->{fname}));')
+    lines.append('printf("macro NC_ELEMENT_F16 %u 0\\n", NC_ELEMENT_F16);')
+    lines.append('printf("macro NC_ELEMENT_BF16 %u 0\\n", NC_ELEMENT_BF16);')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    seen = {}
+    for line in filter(None, out):
+        cname, fname, a, b = line.split()
+        seen[(cname, fname)] = (int(a), int(b))
+    assert seen[("macro", "NC_ELEMENT_F16")][0] == nc.ELEMENT_TYPES["f16"]
+    assert seen[("macro", "NC_ELEMENT_BF16")][0] == nc.ELEMENT_TYPES["bf16"]
+    for cname, py in _ABI_STRUCTS.items():
+        assert seen[(cname, "-")] == (ctypes.sizeof(py), ctypes.alignment(py)), cname
+        for fname, ftype in py._fields_:
+            assert seen[(cname, fname)] == (getattr(py, fname).offset, ctypes.sizeof(ftype)), (cname, fname)
+
+
+def test_options_fields_a_binding_sets():
+    """What a binding's toC (INTEGRATION.md's Zig sketch: nc_flash_options_init, then every field,
+    causal as @intFromBool) relies on: element_type defaults to f16, causal 1 selects the causal
+    kernel and 0 the non-causal one, bf16 selects the _bf16 twin."""
+    o = nc.FlashOptions()
+    nc.load_library().nc_flash_options_init(ctypes.byref(o))
+    assert o.element_type == nc.ELEMENT_TYPES["f16"]
+    base = CONFIGS["c3"].options()
+    for flag, want in ((1, True), (0, False)):
+        base.causal = flag
+        name = nc.select_kernel(base).name.decode()
+        assert name.endswith("_causal") == want, (flag, name)
+    base.element_type = nc.ELEMENT_TYPES["bf16"]
+    assert nc.select_kernel(base).name.decode().endswith("_bf16")
