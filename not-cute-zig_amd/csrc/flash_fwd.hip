@@ -1537,6 +1537,37 @@ extern "C" __global__ __launch_bounds__(256) void nc_util_copy_b128(const u32x4 
 // times the fixed per-launch dispatch and completion cost that no kernel body can remove.
 extern "C" __global__ __launch_bounds__(1024) void nc_util_empty(nc_flash_kernel_args a) { (void)a; }
 
+// MFMA ceiling: back-to-back f16 32x32x16 MFMAs on four independent accumulators per wave, with
+// operands read once from `ops` (n8 half8 elements). Launched with one 768-thread workgroup per CU:
+// 3 waves per SIMD ran this stream fastest (4 waves per SIMD ran it 10-17 % slower), and a second
+// workgroup does not fit beside it, so every CU holds the same work. Under full load the chip's clock falls with
+// the power that the operands' toggling bits draw, so with operands drawn like a workload's inputs
+// this measures the matrix-core rate the chip sustains on such data. out[t] = the sum of thread t's
+// accumulators: 2048 * iters when every operand is 1.0.
+extern "C" __global__ __launch_bounds__(768) void nc_util_mfma_ceiling(const half8 *ops, uint32_t n8, float *out,
+                                                                      uint32_t iters) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    half8 a[4], b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        a[j] = ops[(8u * t + j) % n8];
+        b[j] = ops[(8u * t + 4u + j) % n8];
+    }
+    floatx16 c[4] = {};
+    for (uint32_t it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = mfma32<false>(a[j], b[j], c[j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = mfma32<false>(a[(j + 1) & 3], b[(j + 1) & 3], c[j]);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s += c[j][e];
+    out[t] = s;
+}
+
 // Each instantiation defines NAME (f16) and NAME_bf16.
 #define NC_FLASH_PIPE_KERNEL(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB)                              \
     extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) {        \

@@ -68,3 +68,28 @@ def test_baselines_command_in_own_process(gpu):
     assert recs and all(tuple(x) == fh.RECORD_KEYS for x in recs)
     assert {x["implementation"] for x in recs} <= set(fh.BASELINE_IMPLS)
     assert any(x["implementation"] == "torch_sdpa_math_f32" and x["correct"] for x in recs)
+
+
+def test_mfma_ceiling_kernel_closed_form(gpu):
+    """The MFMA-ceiling kernel that bench.py times: with every operand 1.0 each 32x32x16 MFMA adds
+    16 to every accumulator element, so each thread's sum is 4 accumulators x 16 elements x 2
+    MFMAs per iteration x 16 = 2048 per iteration, exactly."""
+    import ctypes
+
+    import numpy as np
+
+    fn = gpu.get_function("nc_util_mfma_ceiling")
+    ones = np.full(64 * 8, 0x3C00, dtype=np.uint16)  # f16 1.0
+    grid, threads, iters = 2, 768, 37
+    ops = nc.DeviceBuffer.from_array(ones)
+    out = nc.DeviceBuffer(grid * threads * 4)
+    try:
+        out.memset(0)
+        fn.launch((grid,), (threads,), [ctypes.c_void_p(ops.ptr), ctypes.c_uint32(len(ones) // 8),
+                                       ctypes.c_void_p(out.ptr), ctypes.c_uint32(iters)])
+        nc.synchronize()
+        got = out.download(np.float32, grid * threads)
+    finally:
+        ops.free()
+        out.free()
+    assert np.all(got == 2048.0 * iters), got[:8]
