@@ -633,6 +633,48 @@ struct PipeCfg {
     static constexpr int MT = D < 32 ? 1 : D / 32;
 };
 
+// Per-wave timeline stamps, compiled only into the timeline code object (-DNC_TIMELINE; the product
+// kernels carry none) and only into the pipelined kernels that use no scratch memory (the pair-split
+// kernels exchange their partials through it). With a.scratch set (bit 0 cleared), each wave writes
+// NC_TIMELINE_WORDS u64 at a.scratch + (block * waves + wave) * NC_TIMELINE_WORDS:
+//   0-3  core-clock counter (s_memtime) at entry, before and after its key loop, and at its end;
+//   4    the same counter after a fixed sleep that follows word 3;
+//   5, 6 the chip-wide 100 MHz counter (s_memrealtime) read right after words 3 and 4, which gives
+//        the wave's clock at its end and places its counter readings on a common timebase (the read
+//        takes ~1 us to return and holds the wave's exit until then, after every other reading);
+//   7    HW_ID (low 32 bits) and XCC_ID (high 32 bits);
+//   8-11 the wave's key block count, query block, head and key-split index;
+//   12   with bit 0 of a.scratch set, the 100 MHz counter at entry (else 0): it gives the wave's
+//        average clock over its life, for kernels long enough that the clock moves, and holds
+//        the wave for the read's ~1 us at its start.
+#define NC_TIMELINE_WORDS 13
+#ifdef NC_TIMELINE
+#define NC_TL_STAMP(var) const uint64_t var = __builtin_amdgcn_s_memtime();
+#define NC_TL_START()                                                                                    \
+    NC_TL_STAMP(tl_entry)                                                                                \
+    const uint64_t tl_rstart = ((uintptr_t)a.scratch & 1) ? __builtin_amdgcn_s_memrealtime() : 0;
+#define NC_TL_END()                                                                                      \
+    if constexpr (!XS) {                                                                                 \
+        const uint64_t tl_end = __builtin_amdgcn_s_memtime(), tl_r0 = __builtin_amdgcn_s_memrealtime();  \
+        __builtin_amdgcn_s_sleep(27);                                                                    \
+        const uint64_t tl_end2 = __builtin_amdgcn_s_memtime(), tl_r1 = __builtin_amdgcn_s_memrealtime(); \
+        if (lane == 0 && a.scratch != nullptr) {                                                         \
+            uint64_t *st = reinterpret_cast<uint64_t *>((uintptr_t)a.scratch & ~(uintptr_t)1) +         \
+                           ((size_t)blockIdx.x * C::NW + (uint32_t)w) * NC_TIMELINE_WORDS;               \
+            st[0] = tl_entry; st[1] = tl_loop0; st[2] = tl_loop1; st[3] = tl_end; st[4] = tl_end2;       \
+            st[5] = tl_r0; st[6] = tl_r1;                                                                \
+            st[7] = __builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11)) |                             \
+                    ((uint64_t)__builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11)) << 32);           \
+            st[8] = (uint64_t)nblk; st[9] = (uint64_t)qblk; st[10] = head; st[11] = (uint64_t)s;         \
+            st[12] = tl_rstart;                                                                          \
+        }                                                                                                \
+    }
+#else
+#define NC_TL_STAMP(var)
+#define NC_TL_START()
+#define NC_TL_END()
+#endif
+
 template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB, bool BF, bool XS = false>
 __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &a) {
     using C = PipeCfg<D, NQ, NS, NSTAGE, SUB>;
@@ -665,6 +707,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
+    NC_TL_START()
     const int c = lane & 31;
     const int hh = lane >> 5;
     const int qg = w / NS;
@@ -1023,6 +1066,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) qf[kk] = -qf[kk];
     }
+    NC_TL_STAMP(tl_loop0)
     for (int blk0 = 0; blk0 < nblk; blk0 += NSTAGE) {
         step(blk0, IC<0>{});
         static_for<1, NSTAGE>([&](auto ic) {
@@ -1031,6 +1075,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         });
     }
 
+    NC_TL_STAMP(tl_loop1)
     constexpr int DC = D / 4;
     float2v *mlb = reinterpret_cast<float2v *>(smem + C::ML_OFF);  // [BM queries][NS splits]
     const float lt = pair_sum(l);
@@ -1174,6 +1219,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             }
             store_o(reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch), res * __builtin_amdgcn_rcpf(den));
         }
+        NC_TL_END()
         return;
     }
 
@@ -1231,6 +1277,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         for (int j = 1; j < NS; ++j) res += parts[j];
         store_o(reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch), res);
     }
+    NC_TL_END()
 }
 
 // ---------------------------------------------------------------------------------------------

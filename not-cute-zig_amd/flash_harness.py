@@ -11,6 +11,7 @@ runner (modal_run.py:34-69), on one MI355X through the C ABI.
     python flash_harness.py profile-flash --counters DIR   # the same under rocprofv3 counter passes
                                                   # (the Nsight Compute run of modal_run.py:108-146)
     python flash_harness.py benchmark-flash       # runFlashBenchmark (src/main.zig:760-766)
+    python flash_harness.py timeline --workload c3    # per-wave timeline of the selected kernel
     python flash_harness.py compare-table FILE... # the baseline-vs-not-cute table (modal_run.py:34-69)
 
 Correctness here is checked against a float64 softmax(scale * Q K^T) V written in this file (the
@@ -28,6 +29,7 @@ import glob
 import json
 import math
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -597,6 +599,118 @@ def compare_table(records: Sequence[Dict]) -> str:
     return "\n".join(lines)
 
 
+TIMELINE_WORDS = 13  # NC_TIMELINE_WORDS in csrc/flash_fwd.hip
+TIMELINE_OBJECT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "flash_fwd_timeline_gfx950.hsaco")
+
+
+def summarize_timeline(stamps: np.ndarray) -> dict:
+    """Per-wave stamps of one launch ([workgroups, waves, TIMELINE_WORDS] u64, the layout written by
+    the timeline code object) -> times in us from the first wave's start. Each wave's core-clock
+    readings are placed on the chip-wide 100 MHz timebase through its 100 MHz reading at the end:
+    with the clock over its life where it also read that counter at entry (word 12), else with its
+    clock at the end (the two readings of both counters it takes there)."""
+    st = stamps.astype(np.float64)
+    anchored = st[..., 12] > 0
+    cyc_per_tick = np.where(anchored, (st[..., 3] - st[..., 0]) / np.where(anchored, st[..., 5] - st[..., 12], 1.0),
+                            (st[..., 4] - st[..., 3]) / (st[..., 6] - st[..., 5]))  # core cycles per 10 ns
+    to_us = lambda word: (st[..., 5] - (st[..., 3] - st[..., word]) / cyc_per_tick) * 0.01  # noqa: E731
+    start, loop0, loop1, end = to_us(0), to_us(1), to_us(2), to_us(3)
+    t0 = start.min()
+    start, loop0, loop1, end = start - t0, loop0 - t0, loop1 - t0, end - t0
+    qblk = st[:, 0, 9].astype(np.int64)
+    blocks = []
+    for b in sorted(set(qblk.tolist())):
+        m = qblk == b
+        blocks.append({"query_block": b, "workgroups": int(m.sum()), "key_blocks": int(st[m][:, :, 8].max()),
+                       "start": [round(float(start[m].min()), 3), round(float(start[m].max()), 3)],
+                       "loop_start": [round(float(loop0[m].mean()), 3), round(float(loop0[m].max()), 3)],
+                       "loop_end": [round(float(loop1[m].mean()), 3), round(float(loop1[m].max()), 3)],
+                       "end": [round(float(end[m].mean()), 3), round(float(end[m].max()), 3)]})
+    heavy = qblk == max(qblk.tolist(), key=lambda b: float(loop1[qblk == b].max() - loop0[qblk == b].min()))
+    cyc = lambda a, b: float((st[heavy][:, :, b] - st[heavy][:, :, a]).mean())  # noqa: E731
+    return {"clock_ghz": round(float(np.median(cyc_per_tick)) / 10.0, 3), "anchor": "start" if anchored.all() else "end",
+            "wave_start_us": [round(float(np.percentile(start, q)), 3) for q in (0, 50, 100)],
+            "span_us": round(float(end.max()), 3),
+            "blocks": blocks,
+            "heaviest_cycles": {"prologue": round(cyc(0, 1)), "key_loop": round(cyc(1, 2)), "epilogue": round(cyc(2, 3))}}
+
+
+def cmd_timeline(args) -> int:
+    """Per-wave timeline of the kernel the workload selects: the timeline code object's copy of it
+    (csrc/flash_fwd.hip built with -DNC_TIMELINE) in the same graph replays of back-to-back launches
+    as bench.py, stamps taken from the last launch. Prints the per-launch time of both copies (the
+    stamped copy is slower by the ~1 us its last chip-clock read holds each wave) and, per query
+    block, when its waves start, enter and leave their key loop and end."""
+    from flash_workloads import CONFIGS
+
+    wl = CONFIGS[args.workload]
+    opts = wl.options()
+    sel = nc.select_kernel(opts)
+    name = sel.name.decode()
+    if sel.scratch_bytes or not re.search(r"_q\d+s\d+p\d", name):
+        print(f"timeline: {name} carries no stamps (only the pipelined kernels without scratch do)", file=sys.stderr)
+        return 2
+    nc.init()
+    product = nc.Module.load_embedded()
+    stamped = nc.Module.load_file(TIMELINE_OBJECT)
+    q, k, v = wl.make_inputs()
+    bufs = [nc.DeviceBuffer.from_array(x) for x in (q, k, v)] + [nc.DeviceBuffer(wl.length("o") * 4)]
+    grid = sel.grid[0] * sel.grid[1] * sel.grid[2]
+    nw = sel.threads // 64
+    words = grid * nw * TIMELINE_WORDS
+    stamp_bufs = [nc.DeviceBuffer(words * 8) for _ in range(2)]
+    stream = nc.Stream()
+    result = {"workload": wl.describe(), "kernel": name, "launches": args.launches}
+    try:
+        for label, mod in (("product", product), ("stamped", stamped)):
+            fn = mod.get_function(name)
+            blocks = []
+            for i in range(2):
+                a = nc.pack_args(opts, sel, *[b.ptr for b in bufs])
+                if label == "stamped":  # alternate buffers; bit 0 asks for the entry reading
+                    a.scratch = stamp_bufs[i].ptr | (1 if args.anchor == "start" else 0)
+                blocks.append(a)
+            graph = nc.Graph.capture(stream, lambda: [fn.launch((grid,), (sel.threads,), [blocks[i % 2]],
+                                                                stream=stream.handle) for i in range(args.launches)])
+            for i in range(args.warmup):
+                graph.launch(stream)
+                if i % 10 == 9:
+                    stream.synchronize()
+            stream.synchronize()
+            ev0, ev1 = nc.Event(), nc.Event()
+            ev0.record(stream.handle)
+            for _ in range(10):
+                graph.launch(stream)
+            ev1.record(stream.handle)
+            ev1.synchronize()
+            result[f"{label}_us_per_launch"] = round(nc.Event.elapsed(ev0, ev1) * 1e3 / (10 * args.launches), 3)
+            ev0.destroy()
+            ev1.destroy()
+            graph.destroy()
+        last = (args.launches - 1) % 2
+        stamps = stamp_bufs[last].download(np.uint64, words).reshape(grid, nw, TIMELINE_WORDS)
+        result.update(summarize_timeline(stamps))
+    finally:
+        for b in bufs + stamp_bufs:
+            b.free()
+        stream.destroy()
+    if args.json:
+        print(json.dumps(result))
+        return 0
+    print(f"{result['workload']} -> {name}: {result['product_us_per_launch']} us per launch "
+          f"({result['stamped_us_per_launch']} us stamped), clock {result['clock_ghz']} GHz, anchored at the "
+          f"wave's {result['anchor']}")
+    ws = result["wave_start_us"]
+    print(f"waves start at {ws[0]} / {ws[1]} / {ws[2]} us (first / median / last); last wave ends at {result['span_us']} us")
+    print(f"{'query block':>11} {'wgs':>4} {'key blocks':>10}  {'loop start':>15}  {'loop end':>15}  {'end':>15}  (us, mean / max)")
+    for b in result["blocks"]:
+        print(f"{b['query_block']:>11} {b['workgroups']:>4} {b['key_blocks']:>10}  {b['loop_start'][0]:>7.2f} / {b['loop_start'][1]:<5.2f}"
+              f"  {b['loop_end'][0]:>7.2f} / {b['loop_end'][1]:<5.2f}  {b['end'][0]:>7.2f} / {b['end'][1]:<5.2f}")
+    h = result["heaviest_cycles"]
+    print(f"heaviest block, core cycles per wave: prologue {h['prologue']}, key loop {h['key_loop']}, epilogue {h['epilogue']}")
+    return 0
+
+
 def cmd_table(args) -> int:
     recs = []
     for path in args.files:
@@ -626,6 +740,14 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     pf.add_argument("--counters", metavar="DIR", default="",
                     help="run under rocprofv3 counter passes, writing them under DIR, and summarise")
     pf.add_argument("--pass-timeout", type=float, default=120.0, help="seconds per profiler pass")
+    tl = sub.add_parser("timeline", help="per-wave timeline of the selected kernel (timeline code object)")
+    tl.add_argument("--workload", default="c3")
+    tl.add_argument("--launches", type=int, default=100, help="launches per graph; stamps come from the last")
+    tl.add_argument("--warmup", type=int, default=300, help="untimed graph replays first")
+    tl.add_argument("--anchor", choices=("end", "start"), default="end",
+                    help="place waves on the chip clock from their end alone (short kernels) or also from a "
+                         "reading at entry (long kernels, whose clock moves; costs ~1 us at each wave's start)")
+    tl.add_argument("--json", action="store_true")
     t = sub.add_parser("compare-table", help="print the baseline table from JSONL files ('-' = stdin)")
     t.add_argument("files", nargs="+")
     args = ap.parse_args(argv)
@@ -633,6 +755,8 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
         return cmd_table(args)
     if args.cmd == "baselines":
         return cmd_baselines(args)
+    if args.cmd == "timeline":
+        return cmd_timeline(args)
     if args.cmd == "profile-flash" and args.counters:
         return cmd_profile_counters(args)  # before any GPU call: the passes are child processes
     nc.init()

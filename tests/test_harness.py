@@ -105,3 +105,54 @@ def test_profile_counter_passes_fit_the_hardware():
         assert sum(c.startswith("SQ_") for c in ctrs) <= 8, name
         assert sum(c.startswith("GRBM_") for c in ctrs) <= 2, name
         assert sum(tcc_cost.get(c, 1) for c in ctrs if c.startswith(("TCC_", "FETCH", "WRITE"))) <= 4, name
+
+
+def _stamps(waves):
+    """Timeline words for waves given as (workgroup, wave, query block, key blocks, clock GHz, counter
+    offset, realtime offset in 10 ns ticks, (start, loop start, loop end, end) in us)."""
+    nwg = 1 + max(w[0] for w in waves)
+    nw = 1 + max(w[1] for w in waves)
+    st = np.zeros((nwg, nw, fh.TIMELINE_WORDS), dtype=np.uint64)
+    for wg, wv, qb, nblk, ghz, c_off, r_off, times in waves:
+        cyc = [int(c_off + t * 1000 * ghz) for t in times]  # core counter at each point
+        r_end = r_off + times[3] * 100                     # chip clock (100 MHz) at the end
+        sleep = int(ghz * 1000)                             # exactly 100 ticks of the chip clock
+        st[wg, wv, :] = [cyc[0], cyc[1], cyc[2], cyc[3], cyc[3] + sleep, int(r_end), int(r_end) + 100,
+                         0, nblk, qb, 0, wv, 0]
+    return st
+
+
+def test_timeline_summary_reconstructs_times():
+    """Waves on different clocks and core counters (as on different XCDs) are placed on one timebase
+    through their end readings; times come out relative to the first wave's start."""
+    waves = [
+        (0, 0, 3, 4, 2.0, 10_000, 50_000, (0.2, 1.0, 4.0, 5.0)),
+        (0, 1, 3, 4, 2.0, 10_000, 50_000, (0.3, 1.1, 4.6, 5.2)),
+        (1, 0, 0, 1, 2.4, 77_777, 50_000, (0.0, 0.9, 1.2, 2.5)),
+        (1, 1, 0, 1, 2.4, 77_777, 50_000, (0.1, 0.8, 1.1, 2.6)),
+    ]
+    r = fh.summarize_timeline(_stamps(waves))
+    assert r["wave_start_us"][0] == 0.0 and r["wave_start_us"][2] == pytest.approx(0.3, abs=2e-3)
+    assert r["span_us"] == pytest.approx(5.2, abs=2e-3)
+    by = {b["query_block"]: b for b in r["blocks"]}
+    assert by[3]["loop_end"] == pytest.approx([4.3, 4.6], abs=2e-3)
+    assert by[3]["end"][1] == pytest.approx(5.2, abs=2e-3) and by[3]["key_blocks"] == 4
+    assert by[0]["loop_start"] == pytest.approx([0.85, 0.9], abs=2e-3)
+    # the heaviest block is the one with the longest key loop; its per-wave cycles at 2.0 GHz
+    assert r["heaviest_cycles"]["key_loop"] == pytest.approx((3.0 + 3.5) / 2 * 2000, abs=2)
+    assert r["heaviest_cycles"]["prologue"] == pytest.approx(0.8 * 2000, abs=2)
+
+
+def test_timeline_summary_start_anchor():
+    """With the entry reading (word 12) each wave's clock is its average over its life: a wave whose
+    clock at the end differs from its average is still placed correctly."""
+    st = _stamps([(0, 0, 1, 2, 2.0, 5_000, 90_000, (0.0, 1.0, 9.0, 10.0)),
+                  (1, 0, 0, 2, 2.0, 9_000, 90_000, (2.0, 3.0, 6.0, 7.0))])
+    for wg, t_start in ((0, 0.0), (1, 2.0)):
+        st[wg, 0, 12] = int(90_000 + t_start * 100)
+        st[wg, 0, 6] = st[wg, 0, 5] + 80  # the end-of-wave clock reads 2.5 GHz: not used when anchored
+    r = fh.summarize_timeline(st)
+    assert r["anchor"] == "start" and r["clock_ghz"] == pytest.approx(2.0, abs=1e-3)
+    by = {b["query_block"]: b for b in r["blocks"]}
+    assert by[0]["start"][0] == pytest.approx(2.0, abs=2e-3) and by[0]["loop_end"][0] == pytest.approx(6.0, abs=2e-3)
+    assert by[1]["end"][0] == pytest.approx(10.0, abs=2e-3)

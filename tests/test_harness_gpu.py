@@ -93,3 +93,20 @@ def test_mfma_ceiling_kernel_closed_form(gpu):
         ops.free()
         out.free()
     assert np.all(got == 2048.0 * iters), got[:8]
+
+
+def test_timeline_command_c3(gpu, capsys):
+    """`flash_harness.py timeline` on c3: every query block's waves start, enter and leave their key
+    loop and end in that order, the heaviest (last) query blocks end last, and the product kernel
+    is the faster of the two copies."""
+    assert fh.main(["timeline", "--workload", "c3", "--launches", "20", "--warmup", "20", "--json"]) == 0
+    r = json.loads(capsys.readouterr().out.strip().splitlines()[-1])
+    assert r["kernel"].startswith("nc_flash_fwd_d64_q1s8p2_causal")
+    assert 1.0 < r["clock_ghz"] < 3.0
+    assert r["product_us_per_launch"] < r["stamped_us_per_launch"]
+    blocks = {b["query_block"]: b for b in r["blocks"]}
+    assert sorted(blocks) == list(range(32)) and all(b["workgroups"] == 8 for b in blocks.values())
+    for b in blocks.values():
+        assert b["start"][0] <= b["loop_start"][0] <= b["loop_end"][0] <= b["end"][0] <= r["span_us"] + 1e-6
+        assert b["key_blocks"] == b["query_block"] // 8 + 1
+    assert blocks[31]["end"][1] > blocks[0]["end"][1]
