@@ -893,17 +893,33 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt) o[mt] = floatx16{};
 
+    // K prefetch (private staging, two stages, one sub-tile per step): a wave's next tile is in the
+    // other ring stage, and its slice has landed by the end of the current step, so the next K
+    // operand is read from LDS right after this tile's PV products are issued and arrives while
+    // they run instead of at the head of the next step.
+#ifndef NC_NO_KPF
+    constexpr bool KPF = PRIV && NSTAGE == 2 && SUB == 1;
+#else
+    constexpr bool KPF = false;
+#endif
+    half8 kpf[D / 16];
+
     // One 32x32 sub-tile of this wave: S^T = K Q^T for its 32 keys (kt0 ..), online softmax, and
-    // O^T += V^T P^T. TOFF is the sub-tile's byte offset in the LDS ring (a compile-time constant).
-    auto tile = [&](const int kt0, auto toff_c) {
+    // O^T += V^T P^T. TOFF is the sub-tile's byte offset in the LDS ring (a compile-time constant);
+    // with K prefetch, NEXT is the next tile's offset and has_next says whether the wave has one.
+    auto tile = [&](const int kt0, auto toff_c, auto next_c, const bool has_next) {
         constexpr int TOFF = decltype(toff_c)::value;
+        constexpr int NEXT = decltype(next_c)::value;
 
         // S^T of the sub-tile.
         floatx16 acc = floatx16{};
         half8 kf[D / 16];
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
-            kf[kk] = lds_load_b128<TOFF>(kaddr[kk]);
+            if constexpr (KPF)
+                kf[kk] = kpf[kk];
+            else
+                kf[kk] = lds_load_b128<TOFF>(kaddr[kk]);
             acc = mfma32<BF>(kf[kk], qf[kk], acc);
         }
         lds_reads_done(kf);
@@ -1007,6 +1023,13 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                 const u32x4 vv = {v4[0][0], v4[0][1], v4[1][0], v4[1][1]};
                 o[mt] = mfma32<BF>(__builtin_bit_cast(half8, vv), pf[ks], o[mt]);
             }
+        if constexpr (KPF) {
+            if (has_next) {
+                wait_vm_only<0>();  // the wave's slice of the next block has landed
+#pragma unroll
+                for (int kk = 0; kk < D / 16; ++kk) kpf[kk] = lds_load_b128<NEXT>(kaddr[kk]);
+            }
+        }
     };
     // One key block: wait for its stage, refill the stage consumed last step, compute this wave's
     // sub-tiles.
@@ -1017,6 +1040,9 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             // results were consumed), so it refills the stage with this block and waits for it.
             if (blk > 0) issue(blk, IC<0>{});
             wait_vm_only<0>();
+        } else if constexpr (KPF) {
+            // this block's slice was waited for before its K was prefetched
+            if (blk + 1 < nblk) issue(blk + 1, IC<(ST + 1) % 2>{});
         } else if constexpr (PRIV) {
             wait_vm_own<C::LPW, NSTAGE - 2>(min(NSTAGE - 2, nblk - 1 - blk));
             if (blk + NSTAGE - 1 < nblk) issue(blk + NSTAGE - 1, IC<(ST + NSTAGE - 1) % NSTAGE>{});
@@ -1042,7 +1068,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         if (!run) return;
         static_for<0, SUB>([&](auto jc) {
             constexpr int TOFF = ST * C::STAGE + 2 * decltype(jc)::value * ROW16;  // sub-tile in the stage
-            tile(kb + 32 * decltype(jc)::value, IC<TOFF>{});
+            tile(kb + 32 * decltype(jc)::value, IC<TOFF>{}, IC<((ST + 1) % NSTAGE) * C::STAGE>{}, blk + 1 < nblk);
             __builtin_amdgcn_sched_barrier(0);  // keep sub-tiles (and steps) apart
         });
     };
@@ -1062,6 +1088,13 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             qf[kk] = *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(qt + SW::slot(32 * qg + c, 2 * kk + hh) * 16));
     }
     tie_regs(qf);
+    if constexpr (KPF) {
+        if (nblk > 0) {
+            wait_vm_only<0>();  // block 0's slice
+#pragma unroll
+            for (int kk = 0; kk < D / 16; ++kk) kpf[kk] = lds_load_b128<0>(kaddr[kk]);
+        }
+    }
     if (neg_q) {
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) qf[kk] = -qf[kk];
