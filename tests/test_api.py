@@ -412,3 +412,21 @@ def test_options_fields_a_binding_sets():
         assert name.endswith("_causal") == want, (flag, name)
     base.element_type = nc.ELEMENT_TYPES["bf16"]
     assert nc.select_kernel(base).name.decode().endswith("_bf16")
+
+
+def test_noalloc_buffer_holds_every_dispatched_pair_split():
+    """nc_flash_launch_noalloc serves pair-split kernels from a static buffer of
+    NC_NOALLOC_SCRATCH_BYTES (4 MiB): every shape the dispatcher routes to them (d=64 causal, at least
+    96 query blocks, at most 256 workgroups) needs at most 64 KB + 128 pairs x 2 slots, so none is
+    refused."""
+    from flash_workloads import Workload
+
+    with open(os.path.join(ROOT, "include", "notcute_flash.h")) as f:
+        m = re.search(r"#define NC_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", f.read())
+    cap = int(m.group(1)) << int(m.group(2))
+    worst = 0
+    for bh in range(1, 9):
+        for s in range(32 * 90, 32 * 260, 32 * 3):
+            sel = nc.select_kernel(Workload("x", bh, s, 64, True, 0.1, (("normal", 0, 1),) * 3).options())
+            worst = max(worst, sel.scratch_bytes)
+    assert 0 < worst <= cap, (worst, cap)
