@@ -562,41 +562,57 @@ BASELINE_IMPLS = ("torch_sdpa_flash", "torch_sdpa_mem_efficient", "torch_sdpa_ma
                   "rocblas_materialized", "cublas_materialized", "cuda_wmma", "cuda_tiled")
 
 
+# The table's columns (header, format spec): the layout of modal_run.py:34-69's printout, kept so
+# that both read alike. TABLE_KEYS are the record fields a row needs.
+TABLE_COLUMNS = (("kernel", "<18"), ("shape", "<40"), ("baseline", "<26"), ("not-cute ms", ">12"),
+                 ("base ms", ">12"), ("speedup", ">9"), ("ok", ">5"))
+TABLE_KEYS = ("kernel", "implementation", "shape", "mean_ms", "correct")
+
+
 def read_records(lines: Iterable[str]) -> List[Dict]:
-    recs = []
-    for line in lines:
-        line = line.strip()
-        if not line.startswith("{"):
+    """Compare records from JSONL mixed with other program output (the way modal_run.py:21-31 reads
+    a remote run's stdout). A line that does not open a JSON object is other output and is passed
+    over; one that opens an object but does not parse, or lacks a field the table needs, is
+    reported on stderr with its line number and left out."""
+    kept = []
+    for number, text in enumerate(lines, 1):
+        text = text.strip()
+        if not text.startswith("{"):
             continue
         try:
-            r = json.loads(line)
+            rec = json.loads(text)
         except json.JSONDecodeError as exc:
-            log(f"skipping malformed JSONL record: {exc}: {line}")
+            log(f"compare-table: line {number} left out, not valid JSON ({exc.msg} at column {exc.colno})")
             continue
-        if "implementation" in r and "shape" in r:
-            recs.append(r)
-    return recs
+        absent = [key for key in TABLE_KEYS if key not in rec]
+        if absent:
+            log(f"compare-table: line {number} left out, no {'/'.join(absent)} field")
+            continue
+        kept.append(rec)
+    return kept
 
 
 def compare_table(records: Sequence[Dict]) -> str:
-    by_case: Dict[Tuple[str, str], Dict[str, Dict]] = {}
-    for r in records:
-        by_case.setdefault((r["kernel"], r["shape"]), {})[r["implementation"]] = r
-    lines = ["=== baselines vs not-cute ===",
-             f"{'kernel':<18} {'shape':<40} {'baseline':<26} {'not-cute ms':>12} {'base ms':>12} {'speedup':>9} {'ok':>5}"]
-    for (kernel, shape), impls in sorted(by_case.items()):
-        mine = impls.get("not_cute")
-        if not mine:
+    """One row per (kernel, shape, baseline) that has both a not-cute record and a record of that
+    baseline (BASELINE_IMPLS order within a case, cases sorted): both mean times, the baseline's
+    time over not-cute's, and "yes" when both records passed their checks."""
+    cases: Dict[Tuple[str, str], Dict[str, Dict]] = {}
+    for rec in records:
+        cases.setdefault((rec["kernel"], rec["shape"]), {})[rec["implementation"]] = rec
+    rows = []
+    for kernel, shape in sorted(cases):
+        impls = cases[(kernel, shape)]
+        ours = impls.get("not_cute")
+        if ours is None:
             continue
-        for impl in BASELINE_IMPLS:
-            base = impls.get(impl)
-            if not base:
-                continue
-            speedup = base["mean_ms"] / mine["mean_ms"] if mine["mean_ms"] else 0.0
-            ok = "yes" if mine["correct"] and base["correct"] else "no"
-            lines.append(f"{kernel:<18} {shape:<40} {impl:<26} {mine['mean_ms']:>12.6f} {base['mean_ms']:>12.6f} "
-                         f"{speedup:>8.2f}x {ok:>5}")
-    return "\n".join(lines)
+        for name in (n for n in BASELINE_IMPLS if n in impls):
+            theirs = impls[name]
+            ratio = theirs["mean_ms"] / ours["mean_ms"] if ours["mean_ms"] else 0.0
+            rows.append((kernel, shape, name, f"{ours['mean_ms']:.6f}", f"{theirs['mean_ms']:.6f}", f"{ratio:.2f}x",
+                         "yes" if ours["correct"] and theirs["correct"] else "no"))
+    header = tuple(title for title, _ in TABLE_COLUMNS)
+    return "\n".join(["=== baselines vs not-cute ==="] +
+                     [" ".join(format(cell, spec) for cell, (_, spec) in zip(row, TABLE_COLUMNS)) for row in (header, *rows)])
 
 
 TIMELINE_WORDS = 13  # NC_TIMELINE_WORDS in csrc/flash_fwd.hip

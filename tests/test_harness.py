@@ -60,13 +60,16 @@ def test_record_fields_and_formulas():
     assert json.loads(line) == rec
 
 
-def test_compare_table_and_reader():
+def test_compare_table_and_reader(capsys):
     mine = fh.make_record("not_cute", "s1", True, 0.010, 0.009, 0.012, 1, 1, 0.0)
     base = fh.make_record("torch_sdpa_flash", "s1", True, 0.030, 0.029, 0.031, 1, 1, 0.001)
     bad = fh.make_record("torch_sdpa_mem_efficient", "s1", False, 0.020, 0.02, 0.02, 1, 1, 0.5)
     lines = [json.dumps(mine), "not json", "{broken", json.dumps(base), json.dumps(bad), json.dumps({"x": 1})]
     recs = fh.read_records(lines)
     assert len(recs) == 3
+    # Other output passes silently; a broken object and one without the table's fields are reported.
+    err = capsys.readouterr().err.splitlines()
+    assert len(err) == 2 and "line 3" in err[0] and "line 6" in err[1] and "mean_ms" in err[1]
     table = fh.compare_table(recs).splitlines()
     flash_row = [r for r in table if "torch_sdpa_flash" in r][0]
     assert "3.00x" in flash_row and flash_row.rstrip().endswith("yes")
