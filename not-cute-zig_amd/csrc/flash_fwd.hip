@@ -897,11 +897,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // other ring stage, and its slice has landed by the end of the current step, so the next K
     // operand is read from LDS right after this tile's PV products are issued and arrives while
     // they run instead of at the head of the next step.
-#ifndef NC_NO_KPF
     constexpr bool KPF = PRIV && NSTAGE == 2 && SUB == 1;
-#else
-    constexpr bool KPF = false;
-#endif
     half8 kpf[D / 16];
 
     // One 32x32 sub-tile of this wave: S^T = K Q^T for its 32 keys (kt0 ..), online softmax, and
