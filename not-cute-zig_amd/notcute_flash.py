@@ -18,7 +18,9 @@ from typing import Optional, Sequence
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libnotcute_flash.so")
+# NC_LIBRARY selects another build of the same library (e.g. the host-sanitizer build of
+# `make host-sanitize`); by default the in-tree one.
+LIB_PATH = os.environ.get("NC_LIBRARY") or os.path.join(HERE, "libnotcute_flash.so")
 
 STATUS_NAMES = [
     "Success", "OutOfMemory", "Overflow", "SharedObjectInitFailed", "NotFound", "InvalidValue",
