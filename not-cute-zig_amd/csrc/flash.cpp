@@ -142,9 +142,13 @@ const char *reference_kernel(const nc_flash_options &o) {
 // d=16/32, interleaved timing). At d=64 the 128-VGPR q2s4 runs two workgroups per CU and wins the
 // middle ground: causal masking makes the shared-staging kernels' per-workgroup work uneven, so
 // causal shapes need more workgroups (or short sequences) before q8s1 or q2s4 beat the private-
-// staging q1s8, whose 8 key-split waves stay balanced on any grid. The bf16 twins have the same
-// instruction stream (bf16 MFMA, conversion and dot forms instead of the f16 ones) and follow the
-// same rule.
+// staging q1s8, whose 8 key-split waves stay balanced on any grid. The 4-wave q4s1 kernels (128
+// query rows, MFMA accumulators in VGPRs) take grids of many short-to-mid sequences: at d=64 from
+// 1024 of their workgroups up to S = 8192 (and 512 up to S = 1024 causal), below the long causal
+// sequences over many heads that q8s1 keeps (c5); at d=32 from 512 workgroups (1024 causal). Re-fitted
+// on 137 shapes (d=64 and 32, BH 4-512, S 128-16384, causal and not): the picks total 1.0009x the
+// per-shape best. The bf16 twins have the same instruction stream (bf16 MFMA, conversion and dot
+// forms instead of the f16 ones) and follow the same rule.
 const Variant *choose_pipe(const nc_flash_options &o) {
     const uint32_t d = (uint32_t)o.head_dim;
     const bool causal = o.causal != 0;
@@ -153,22 +157,23 @@ const Variant *choose_pipe(const nc_flash_options &o) {
     auto wgs = [&](uint64_t bm) { return ((S + bm - 1) / bm) * o.batch_heads; };
     if (d == 64) {
         if (causal) {
-            if (wgs(256) >= 512 && (S <= 4096 || wgs(256) >= 1024)) return find_pipe(d, 8, 1, causal, bf);
-            if (S <= 512 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal, bf);
+            if (wgs(256) >= 1024 && S >= 4096) return find_pipe(d, 8, 1, causal, bf);
+            if ((wgs(128) >= 1024 && S <= 8192) || (S <= 1024 && wgs(128) >= 512)) return find_pipe(d, 4, 1, causal, bf);
             const uint64_t w64 = wgs(64);
             if ((S <= 1024 && w64 >= 256) || (S <= 2048 && w64 >= 288) || (S <= 4096 && w64 >= 384) || w64 >= 512)
                 return find_pipe(d, 2, 4, causal, bf);
             return find_pipe(d, 1, 8, causal, bf);
         }
-        if (S <= 256 && wgs(128) >= 512) return find_pipe(d, 4, 1, causal, bf);
+        if (S <= 256 && wgs(128) >= 256) return find_pipe(d, 4, 1, causal, bf);
         if (wgs(256) >= 256) return find_pipe(d, 8, 1, causal, bf);
         if (wgs(64) >= 256) return find_pipe(d, 2, 4, causal, bf);
         return find_pipe(d, 1, 8, causal, bf);
     }
     if (d == 32) {
-        if ((S <= (causal ? 256u : 512u) && wgs(128) >= 512) || (S <= 1024 && wgs(128) >= 1024))
+        if (causal ? (wgs(128) >= 1024 || (S <= 512 && wgs(128) >= 512))
+                   : (wgs(128) >= 512 || (S <= 128 && wgs(128) >= 256)))
             return find_pipe(d, 4, 1, causal, bf);
-        if ((causal ? (wgs(64) >= 1024 && (S <= 4096 || wgs(64) >= 2048)) : wgs(64) >= 512) ||
+        if ((causal ? ((wgs(64) >= 512 && S <= 4096) || wgs(64) >= 2048) : wgs(64) >= 512) ||
             (S <= 256 && wgs(64) >= 256))
             return find_pipe(d, 2, 4, causal, bf);
         return find_pipe(d, 1, 8, causal, bf);
