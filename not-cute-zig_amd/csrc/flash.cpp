@@ -73,8 +73,9 @@ struct Variant {
     PIPE2(64, 4, 1, 2, "causal", T, BF), PIPE(64, 2, 4, 2, "full", T, BF), PIPE(64, 2, 4, 2, "causal", T, BF),  \
     PIPE(64, 1, 8, 2, "full", T, BF), PIPE(64, 1, 8, 2, "causal", T, BF), PIPE(32, 4, 1, 3, "full", T, BF),     \
     PIPE(32, 4, 1, 3, "causal", T, BF), PIPE(32, 2, 4, 2, "full", T, BF), PIPE(32, 2, 4, 2, "causal", T, BF),   \
-    PIPE(32, 1, 8, 2, "full", T, BF), PIPE(32, 1, 8, 2, "causal", T, BF), PIPE(16, 2, 4, 2, "full", T, BF),     \
-    PIPE(16, 2, 4, 2, "causal", T, BF), PIPE(16, 1, 8, 2, "full", T, BF), PIPE(16, 1, 8, 2, "causal", T, BF),   \
+    PIPE(32, 1, 8, 2, "full", T, BF), PIPE(32, 1, 8, 2, "causal", T, BF), PIPE2(16, 4, 1, 2, "full", T, BF),    \
+    PIPE2(16, 4, 1, 2, "causal", T, BF), PIPE(16, 2, 4, 2, "full", T, BF), PIPE(16, 2, 4, 2, "causal", T, BF),  \
+    PIPE(16, 1, 8, 2, "full", T, BF), PIPE(16, 1, 8, 2, "causal", T, BF),                                      \
     GEN(16, "full", true, "", T, BF), GEN(16, "causal", true, "", T, BF), GEN(32, "full", true, "", T, BF),     \
     GEN(32, "causal", true, "", T, BF), GEN(64, "full", true, "", T, BF), GEN(64, "causal", true, "", T, BF),   \
     GEN(16, "full", false, "_unaligned", T, BF), GEN(16, "causal", false, "_unaligned", T, BF),                \
@@ -178,9 +179,11 @@ const Variant *choose_pipe(const nc_flash_options &o) {
             return find_pipe(d, 2, 4, causal, bf);
         return find_pipe(d, 1, 8, causal, bf);
     }
-    // d = 16: long sequences over few heads keep the 8 key splits unless the grid is large.
-    if ((wgs(64) >= 1024 && (S <= 4096 || wgs(64) >= 2048)) || (S <= 256 && wgs(64) >= 256))
-        return find_pipe(d, 2, 4, causal, bf);
+    // d = 16: the workgroups a kernel needs grow with the sequence (longer key loops per workgroup);
+    // q4s1 (two 32-key sub-tiles per block) from 384-1536 of its workgroups, then q2s4 from 192-768.
+    const uint64_t w128 = wgs(128), w64 = wgs(64);
+    if (w128 >= (S <= 512 ? 384u : S <= (causal ? 2048u : 1024u) ? 768u : 1536u)) return find_pipe(d, 4, 1, causal, bf);
+    if (w64 >= (S <= (causal ? 512u : 256u) ? 192u : S <= 1024 ? 384u : 768u)) return find_pipe(d, 2, 4, causal, bf);
     return find_pipe(d, 1, 8, causal, bf);
 }
 

@@ -1688,6 +1688,8 @@ NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_full, 32, 2, 4, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q2s4p2_causal, 32, 2, 4, true, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p2_full, 32, 1, 8, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p2_causal, 32, 1, 8, true, 2, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q4s1p2t2_full, 16, 4, 1, false, 2, 2)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q4s1p2t2_causal, 16, 4, 1, true, 2, 2)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_full, 16, 2, 4, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_causal, 16, 2, 4, true, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_full, 16, 1, 8, false, 2, 1)
