@@ -81,11 +81,15 @@ int nc_device_count(int *count);
 /* cuCtxSynchronize equivalent. */
 int nc_device_synchronize(void);
 
-/* cuda.malloc / free / memcpy (src/cuda.zig:259-290). Sizes are in bytes. */
+/* cuda.malloc / free / memcpy (src/cuda.zig:259-290). Sizes are in bytes. Both copies return once
+ * the bytes are at their destination, so work submitted afterwards to any stream sees them. */
 int nc_malloc(void **dptr, size_t bytes);
 void nc_free(void *dptr);
 int nc_memcpy_htod(void *dst_device, const void *src_host, size_t bytes);
 int nc_memcpy_dtoh(void *dst_host, const void *src_device, size_t bytes);
+/* Fills `bytes` bytes with `byte_value` and returns once the fill is complete, so work submitted
+ * afterwards to any stream (streams here are non-blocking) sees it. An extension: the reference
+ * clears its host arrays before copying them over (src/main.zig:994-995). */
 int nc_memset(void *dst_device, int byte_value, size_t bytes);
 
 /* Module (src/cuda.zig:293-316). */

@@ -155,16 +155,25 @@ void nc_free(void *dptr) {
     if (st) std::fprintf(stderr, "not-cute: failed to free device memory: %s\n", nc_status_name(st));
 }
 
+// A copy from pageable host memory may return once the bytes are staged, before they reach the
+// device, and it is ordered only on the null stream: waited for here, so kernels launched next on
+// any stream read the copied bytes.
 int nc_memcpy_htod(void *dst, const void *src, size_t bytes) {
-    return check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy(HtoD)");
+    int st = check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy(HtoD)");
+    if (st) return st;
+    return check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
 }
 
 int nc_memcpy_dtoh(void *dst, const void *src, size_t bytes) {
     return check(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy(DtoH)");
 }
 
+// The fill runs on the null stream, which the library's non-blocking streams do not wait for, so
+// it is waited for here: work submitted afterwards to any stream sees the filled bytes.
 int nc_memset(void *dst, int byte_value, size_t bytes) {
-    return check(hipMemset(dst, byte_value, bytes), "hipMemset");
+    int st = check(hipMemset(dst, byte_value, bytes), "hipMemset");
+    if (st) return st;
+    return check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
 }
 
 static int module_from(hipModule_t m, nc_module *out) {

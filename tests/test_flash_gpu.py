@@ -132,6 +132,62 @@ def test_every_kernel_variant(gpu):
     assert len(seen) >= 6
 
 
+def test_memset_done_before_stream_work(gpu):
+    """nc_memset returns once the fill is complete: a kernel launched right after it on a
+    non-blocking stream (which does not wait for the null stream the fill runs on) writes over the
+    filled bytes, and its writes are what stays. 512 MiB make a late fill overwrite them."""
+    import ctypes
+
+    big_bytes, n16 = 512 << 20, 64
+    src_words = np.arange(n16 * 4, dtype=np.uint32) + 1
+    src = nc.DeviceBuffer.from_array(src_words)
+    big = nc.DeviceBuffer(big_bytes)
+    stream = nc.Stream()
+    fn = gpu.get_function("nc_util_copy_b128")
+    try:
+        for rep in range(3):
+            say(f"[case] memset 512 MiB then copy on a non-blocking stream, rep {rep}")
+            big.memset(0xFF)
+            fn.launch((1,), (256,), [ctypes.c_void_p(src.ptr), ctypes.c_void_p(big.ptr), ctypes.c_uint64(n16)],
+                      stream=stream.handle)
+            stream.synchronize()
+            head = big.download(np.uint32, n16 * 4)
+            tail = big.download(np.uint32, 64, big_bytes - 256)
+            assert np.array_equal(head, src_words), f"rep {rep}: the fill landed after the copy"
+            assert np.all(tail == 0xFFFFFFFF), f"rep {rep}: the fill did not reach the end"
+    finally:
+        stream.destroy()
+        src.free()
+        big.free()
+
+
+def test_upload_done_before_stream_work(gpu):
+    """nc_memcpy_htod returns once the bytes are on the device: a kernel launched right after it on
+    a non-blocking stream reads the uploaded tail of a 512 MiB pageable-host copy."""
+    import ctypes
+
+    n16 = 64
+    host = np.empty((512 << 20) // 4, dtype=np.uint32)
+    dst = nc.DeviceBuffer(n16 * 16)
+    stream = nc.Stream()
+    fn = gpu.get_function("nc_util_copy_b128")
+    big = nc.DeviceBuffer(host.nbytes)
+    try:
+        for rep in range(3):
+            say(f"[case] upload 512 MiB then copy its tail on a non-blocking stream, rep {rep}")
+            host[:] = np.uint32(0x01010101 * (rep + 1))
+            big.upload(host)
+            fn.launch((1,), (256,), [ctypes.c_void_p(big.ptr + host.nbytes - n16 * 16), ctypes.c_void_p(dst.ptr),
+                                     ctypes.c_uint64(n16)], stream=stream.handle)
+            stream.synchronize()
+            got = dst.download(np.uint32, n16 * 4)
+            assert np.all(got == np.uint32(0x01010101 * (rep + 1))), f"rep {rep}: the kernel read before the upload"
+    finally:
+        stream.destroy()
+        dst.free()
+        big.free()
+
+
 def test_launch_rejects_short_buffers(gpu):
     wl = CONFIGS["c1"]
     q, k, v = wl.make_inputs()
