@@ -12,6 +12,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <limits>
@@ -135,56 +136,94 @@ const char *reference_kernel(const nc_flash_options &o) {
     return "flash_attention_fwd_opt";
 }
 
-// MI355X dispatch (256 CUs). Wider query blocks share every staged K/V tile among more waves, so
-// they are preferred once the grid gives every CU enough workgroups; short or few sequences move to
-// narrower query blocks whose keys are split over more waves, so that even the heaviest (causal:
-// last) query block finishes in a few key-block steps.
-// Chosen from GPU sweeps of every variant over BH x S x d x causal (102 shapes for d=64, 56 for
-// d=16/32, interleaved timing). At d=64 the 128-VGPR q2s4 runs two workgroups per CU and wins the
-// middle ground: causal masking makes the shared-staging kernels' per-workgroup work uneven, so
-// causal shapes need more workgroups (or short sequences) before q8s1 or q2s4 beat the private-
-// staging q1s8, whose 8 key-split waves stay balanced on any grid. The 4-wave q4s1 kernels (128
-// query rows, MFMA accumulators in VGPRs) take grids of many short-to-mid sequences: at d=64 from
-// 1024 of their workgroups up to S = 8192 (and 512 up to S = 1024 causal), below the long causal
-// sequences over many heads that q8s1 keeps (c5); at d=32 from 512 workgroups (1024 causal). Re-fitted
-// on 137 shapes (d=64 and 32, BH 4-512, S 128-16384, causal and not): the picks total 1.0009x the
-// per-shape best. The bf16 twins have the same instruction stream (bf16 MFMA, conversion and dot
-// forms instead of the f16 ones) and follow the same rule.
+// MI355X dispatch (256 CUs): every pipelined kernel of the head size is priced by a cost model and
+// the cheapest is launched. A kernel's workgroups are dealt to the CUs in block order (heaviest
+// causal query blocks first), so the busiest CU holds workgroups 0, 256, 512, ... . It runs up to
+// wg_per_cu of them at once (from each kernel's registers and LDS); each resident workgroup needs
+// rho + steps units of work, steps being its busiest wave's sequential 32-key tiles (the padded key
+// blocks up to its last visible key), and advances one unit per max(lat, k * waves_per_simd * tau)
+// us while k workgroups share the CU: lat is one wave's latency-bound tile, tau a tile's share of a
+// SIMD once waves interleave. The estimate is a + that CU's finishing time. Partial query and key
+// blocks, causal imbalance and how full the CUs are all enter through the steps and the sharing,
+// which fixed grid-size thresholds miss off a power-of-two grid. (a, rho, lat, tau) were fitted per
+// kernel to interleaved GPU timings of every variant on 245 (d=64), 244 (d=32) and 298 (d=16)
+// shapes (BH 1-1024, S 64-16384, causal and not; a grid, an off-grid set and a random set). In
+// three-fold cross-validation the picks average 1.012x (d=64), 1.006x (d=32) and 1.010x (d=16)
+// the per-shape best; on the random set the threshold rule they replace averaged 1.047x, 1.028x
+// and 1.008x. The bf16 twins have the same instruction stream and use the same model.
+struct PipeModel {
+    uint32_t d, nq, ns, wg_per_cu, waves_per_simd;
+    float a, rho, lat, tau;
+};
+const PipeModel kPipeModels[] = {
+    {64, 8, 1, 2, 2, 2.3643f, 3.7198f, 0.5110f, 0.2491f},  // q8s1p2t2
+    {64, 4, 1, 4, 1, 1.9664f, 4.3401f, 0.4105f, 0.2735f},  // q4s1p2t2
+    {64, 2, 4, 2, 2, 2.0057f, 2.5877f, 0.5000f, 0.3134f},  // q2s4p2
+    {64, 1, 8, 1, 2, 0.4023f, 2.9534f, 0.3000f, 0.3978f},  // q1s8p2
+    {32, 4, 1, 5, 1, 2.0217f, 2.5512f, 0.3837f, 0.1863f},  // q4s1p3
+    {32, 2, 4, 2, 2, 1.7707f, 2.6393f, 0.5084f, 0.2020f},  // q2s4p2
+    {32, 1, 8, 2, 2, 1.6322f, 1.5959f, 0.5621f, 0.2483f},  // q1s8p2
+    {16, 4, 1, 6, 1, 2.2710f, 1.9930f, 0.3234f, 0.1546f},  // q4s1p2t2
+    {16, 2, 4, 3, 2, 2.0612f, 2.0224f, 0.4410f, 0.1567f},  // q2s4p2
+    {16, 1, 8, 2, 2, 1.7206f, 1.9272f, 0.4156f, 0.1693f},  // q1s8p2
+};
+
+// Sequential 32-key tiles of the busiest wave of query block qb.
+uint64_t pipe_steps(const Variant &v, uint64_t S, bool causal, uint64_t qb) {
+    const uint64_t kv = causal ? std::min<uint64_t>(S, (qb + 1) * v.bm()) : S;
+    if (v.nq == 1) return ((kv + 31) / 32 + v.ns - 1) / v.ns;  // private staging: wave s takes tiles s + ns*i
+    return (kv + v.bn() - 1) / v.bn() * v.sub;
+}
+
+double pipe_cost(const PipeModel &m, const Variant &v, uint64_t batch_heads, uint64_t S, bool causal) {
+    const uint64_t nqb = (S + v.bm() - 1) / v.bm(), n = nqb * batch_heads, ncu = (n + 255) / 256;
+    auto per = [&](uint64_t k) { return std::max<double>(m.lat, (double)k * m.waves_per_simd * m.tau); };
+    if (!causal) {  // equal workgroups: rounds of wg_per_cu, then the remainder
+        const double job = (double)pipe_steps(v, S, false, 0) + m.rho;
+        const uint64_t full = ncu / m.wg_per_cu, rem = ncu % m.wg_per_cu;
+        return m.a + job * ((double)full * per(m.wg_per_cu) + (rem ? per(rem) : 0.0));
+    }
+    auto job = [&](uint64_t i) { return (double)pipe_steps(v, S, true, nqb - 1 - (256 * i) / batch_heads) + m.rho; };
+    double t = 0.0;
+    if (ncu > 512) {  // the CU stays full but for a short tail: its 1/256 share of all the work
+        for (uint64_t qb = 0; qb < nqb; ++qb) t += (double)pipe_steps(v, S, true, qb);
+        t = t * (double)batch_heads / 256.0 + (double)ncu * m.rho;
+        return m.a + t * per(m.wg_per_cu) / m.wg_per_cu;
+    }
+    double act[8];
+    uint32_t na = 0;
+    uint64_t i = 0;
+    for (;;) {
+        while (na < m.wg_per_cu && i < ncu) act[na++] = job(i++);
+        if (na == 0) break;
+        double mn = act[0];
+        for (uint32_t r = 1; r < na; ++r) mn = std::min(mn, act[r]);
+        t += mn * per(na);
+        uint32_t k = 0;
+        for (uint32_t r = 0; r < na; ++r)
+            if (act[r] - mn > 1e-9) act[k++] = act[r] - mn;
+        na = k;
+    }
+    return m.a + t;
+}
+
 const Variant *choose_pipe(const nc_flash_options &o) {
     const uint32_t d = (uint32_t)o.head_dim;
     const bool causal = o.causal != 0;
     const bool bf = o.element_type == NC_ELEMENT_BF16;
-    const uint64_t S = o.seq_len;
-    auto wgs = [&](uint64_t bm) { return ((S + bm - 1) / bm) * o.batch_heads; };
-    if (d == 64) {
-        if (causal) {
-            if (wgs(256) >= 1024 && S >= 4096) return find_pipe(d, 8, 1, causal, bf);
-            if ((wgs(128) >= 1024 && S <= 8192) || (S <= 1024 && wgs(128) >= 512)) return find_pipe(d, 4, 1, causal, bf);
-            const uint64_t w64 = wgs(64);
-            if ((S <= 1024 && w64 >= 256) || (S <= 2048 && w64 >= 288) || (S <= 4096 && w64 >= 384) || w64 >= 512)
-                return find_pipe(d, 2, 4, causal, bf);
-            return find_pipe(d, 1, 8, causal, bf);
+    const Variant *best = nullptr;
+    double best_t = 0.0;
+    for (const auto &m : kPipeModels) {
+        if (m.d != d) continue;
+        const Variant *v = find_pipe(d, m.nq, m.ns, causal, bf);
+        if (!v) continue;
+        const double t = pipe_cost(m, *v, o.batch_heads, o.seq_len, causal);
+        if (!best || t < best_t) {
+            best = v;
+            best_t = t;
         }
-        if (S <= 256 && wgs(128) >= 256) return find_pipe(d, 4, 1, causal, bf);
-        if (wgs(256) >= 256) return find_pipe(d, 8, 1, causal, bf);
-        if (wgs(64) >= 256) return find_pipe(d, 2, 4, causal, bf);
-        return find_pipe(d, 1, 8, causal, bf);
     }
-    if (d == 32) {
-        if (causal ? (wgs(128) >= 1024 || (S <= 512 && wgs(128) >= 512))
-                   : (wgs(128) >= 512 || (S <= 128 && wgs(128) >= 256)))
-            return find_pipe(d, 4, 1, causal, bf);
-        if ((causal ? ((wgs(64) >= 512 && S <= 4096) || wgs(64) >= 2048) : wgs(64) >= 512) ||
-            (S <= 256 && wgs(64) >= 256))
-            return find_pipe(d, 2, 4, causal, bf);
-        return find_pipe(d, 1, 8, causal, bf);
-    }
-    // d = 16: the workgroups a kernel needs grow with the sequence (longer key loops per workgroup);
-    // q4s1 (two 32-key sub-tiles per block) from 384-1536 of its workgroups, then q2s4 from 192-768.
-    const uint64_t w128 = wgs(128), w64 = wgs(64);
-    if (w128 >= (S <= 512 ? 384u : S <= (causal ? 2048u : 1024u) ? 768u : 1536u)) return find_pipe(d, 4, 1, causal, bf);
-    if (w64 >= (S <= (causal ? 512u : 256u) ? 192u : S <= 1024 ? 384u : 768u)) return find_pipe(d, 2, 4, causal, bf);
-    return find_pipe(d, 1, 8, causal, bf);
+    return best;
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -321,6 +321,41 @@ def test_code_object_exports_reference_kernel_symbols():
     assert b"\0flash_attention_fwd\0" in blob
 
 
+# (head_dim, batch_heads, seq_len, causal): the kernel that beat every other pipelined variant in
+# interleaved GPU timings of all of them (f16, one MI355X), with its time and the runner-up's ratio.
+# Off-grid shapes from the validation sweeps, two per kernel and head size.
+MEASURED_WINNERS = [
+    ((16, 1, 8687, True), "q1s8p2"),  # 17.2 us, next 1.99x
+    ((16, 1, 5753, True), "q1s8p2"),  # 11.9 us, next 1.98x
+    ((16, 48, 1536, True), "q2s4p2"),  # 13.8 us, next 1.27x
+    ((16, 62, 571, True), "q2s4p2"),  # 6.4 us, next 1.23x
+    ((16, 768, 384, True), "q4s1p2t2"),  # 16.1 us, next 1.57x
+    ((16, 751, 110, True), "q4s1p2t2"),  # 5.7 us, next 1.46x
+    ((32, 1, 6536, True), "q1s8p2"),  # 15.0 us, next 1.99x
+    ((32, 1, 4811, False), "q1s8p2"),  # 12.0 us, next 1.94x
+    ((32, 29, 1919, True), "q2s4p2"),  # 19.0 us, next 1.25x
+    ((32, 48, 768, True), "q2s4p2"),  # 8.1 us, next 1.21x
+    ((32, 973, 87, False), "q4s1p3"),  # 6.6 us, next 2.22x
+    ((32, 780, 65, False), "q4s1p3"),  # 5.9 us, next 2.09x
+    ((64, 1, 5399, False), "q1s8p2"),  # 17.5 us, next 1.78x
+    ((64, 4, 2351, True), "q1s8p2"),  # 9.5 us, next 1.63x
+    ((64, 48, 384, True), "q2s4p2"),  # 6.3 us, next 1.44x
+    ((64, 24, 1536, True), "q2s4p2"),  # 15.8 us, next 1.40x
+    ((64, 776, 91, True), "q4s1p2t2"),  # 9.0 us, next 1.68x
+    ((64, 926, 80, True), "q4s1p2t2"),  # 9.5 us, next 1.66x
+    ((64, 406, 190, False), "q8s1p2t2"),  # 11.8 us, next 1.29x
+    ((64, 441, 130, False), "q8s1p2t2"),  # 11.2 us, next 1.12x
+]
+
+
+@pytest.mark.parametrize("case,kernel", MEASURED_WINNERS)
+def test_dispatch_picks_measured_winner(case, kernel):
+    d, bh, s, causal = case
+    for dtype in ("f16", "bf16"):
+        name = nc.select_kernel(nc.options(batch_heads=bh, seq_len=s, head_dim=d, causal=causal, dtype=dtype)).name
+        assert f"_{kernel}_" in name.decode(), (case, dtype, name)
+
+
 def test_pair_split_dispatch_region():
     """The pair-split kernel replaces the private-staging one for d=64 causal shapes with at least 96
     query blocks whose grid fits one workgroup per CU (measured faster there, slower elsewhere)."""
