@@ -136,8 +136,8 @@ const char *reference_kernel(const nc_flash_options &o) {
     return "flash_attention_fwd_opt";
 }
 
-// MI355X dispatch (256 CUs): every pipelined kernel of the head size is priced by a cost model and
-// the cheapest is launched. A kernel's workgroups are dealt to the CUs in block order (heaviest
+// MI355X dispatch (256 CUs): at d = 64 and 32 every pipelined kernel of the head size is priced by a
+// cost model and the cheapest is launched (d = 16: fitted thresholds, in choose_pipe). A kernel's workgroups are dealt to the CUs in block order (heaviest
 // causal query blocks first), so the busiest CU holds workgroups 0, 256, 512, ... . It runs up to
 // wg_per_cu of them at once (from each kernel's registers and LDS); each resident workgroup needs
 // rho + steps units of work, steps being its busiest wave's sequential 32-key tiles (the padded key
@@ -146,11 +146,12 @@ const char *reference_kernel(const nc_flash_options &o) {
 // SIMD once waves interleave. The estimate is a + that CU's finishing time. Partial query and key
 // blocks, causal imbalance and how full the CUs are all enter through the steps and the sharing,
 // which fixed grid-size thresholds miss off a power-of-two grid. (a, rho, lat, tau) were fitted per
-// kernel to interleaved GPU timings of every variant on 245 (d=64), 244 (d=32) and 298 (d=16)
-// shapes (BH 1-1024, S 64-16384, causal and not; a grid, an off-grid set and a random set). In
-// three-fold cross-validation the picks average 1.012x (d=64), 1.006x (d=32) and 1.010x (d=16)
-// the per-shape best; on the random set the threshold rule they replace averaged 1.047x, 1.028x
-// and 1.008x. The bf16 twins have the same instruction stream and use the same model.
+// kernel to interleaved GPU timings of every variant on 245 (d=64) and 244 (d=32) shapes (BH 1-1024,
+// S 64-16384, causal and not; a grid, an off-grid set and a random set). On 100 random shapes per
+// head size timed after the fit the picks average 1.003x (d=64) and 1.006x (d=32) the per-shape
+// best, where the threshold rules they replace averaged 1.052x and 1.023x; on 50 bf16 shapes each,
+// 1.010x and 1.006x (thresholds: 1.046x and 1.049x). The bf16 twins have the same instruction
+// stream and use the same model.
 struct PipeModel {
     uint32_t d, nq, ns, wg_per_cu, waves_per_simd;
     float a, rho, lat, tau;
@@ -163,9 +164,6 @@ const PipeModel kPipeModels[] = {
     {32, 4, 1, 5, 1, 2.0217f, 2.5512f, 0.3837f, 0.1863f},  // q4s1p3
     {32, 2, 4, 2, 2, 1.7707f, 2.6393f, 0.5084f, 0.2020f},  // q2s4p2
     {32, 1, 8, 2, 2, 1.6322f, 1.5959f, 0.5621f, 0.2483f},  // q1s8p2
-    {16, 4, 1, 6, 1, 2.2710f, 1.9930f, 0.3234f, 0.1546f},  // q4s1p2t2
-    {16, 2, 4, 3, 2, 2.0612f, 2.0224f, 0.4410f, 0.1567f},  // q2s4p2
-    {16, 1, 8, 2, 2, 1.7206f, 1.9272f, 0.4156f, 0.1693f},  // q1s8p2
 };
 
 // Sequential 32-key tiles of the busiest wave of query block qb.
@@ -211,6 +209,17 @@ const Variant *choose_pipe(const nc_flash_options &o) {
     const uint32_t d = (uint32_t)o.head_dim;
     const bool causal = o.causal != 0;
     const bool bf = o.element_type == NC_ELEMENT_BF16;
+    if (d == 16) {
+        // d = 16 tiles are cheap next to their softmax and staging, and the model above picks worse
+        // there (1.010x the per-shape best in cross-validation) than these fitted thresholds
+        // (1.008-1.011x on two random sets timed after their fit, f16 and bf16): q4s1 from 384-1536 of
+        // its workgroups, more for longer sequences, then q2s4 from 192-768 of its own.
+        const uint64_t S = o.seq_len, bh = o.batch_heads;
+        const uint64_t w128 = (S + 127) / 128 * bh, w64 = (S + 63) / 64 * bh;
+        if (w128 >= (S <= 512 ? 384u : S <= (causal ? 2048u : 1024u) ? 768u : 1536u)) return find_pipe(d, 4, 1, causal, bf);
+        if (w64 >= (S <= (causal ? 512u : 256u) ? 192u : S <= 1024 ? 384u : 768u)) return find_pipe(d, 2, 4, causal, bf);
+        return find_pipe(d, 1, 8, causal, bf);
+    }
     const Variant *best = nullptr;
     double best_t = 0.0;
     for (const auto &m : kPipeModels) {
