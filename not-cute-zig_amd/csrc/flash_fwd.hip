@@ -1422,7 +1422,16 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
             *reinterpret_cast<NC_LDS(u32x4) *>((uintptr_t)(vst + off)) = vreg[j];
         }
     };
-    if (VEC && w < nch) fetch(w);
+    // Two chunk streams per wave (VEC, at most two waves: the reference's 64- and 128-thread
+    // launches, on slices that fit 32-bit buffer offsets). One wave per SIMD has nothing else to hide
+    // a chunk's serial chain of LDS round trips, MFMAs and cross-lane reductions, so each wave keeps
+    // two online-softmax states, A over its chunks w, w + 2NW, ... and B over w + NW, w + 3NW, ...,
+    // runs the two chains side by side in one branch-free body and merges them after the loop. Each
+    // stream stages in its own region (the two regions of a wave are the ones two more waves would
+    // use), and the next pair's rows are fetched by range-checked buffer loads, which read zero past
+    // the slice.
+    const bool pair = VEC && NW <= 2 && (uint64_t)S * D * 2 < (1ull << 31);
+    if (VEC && !pair && w < nch) fetch(w);
 
     const float sc = scale * kLog2e;
     float mrow = neg_inf(), l = 0.f;
@@ -1431,7 +1440,142 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
     for (int dt = 0; dt < DT; ++dt) oacc[dt] = floatx4{};
     const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-    for (int ch = w; ch < nch; ch += NW) {
+    if constexpr (VEC) {
+        if (pair) {
+            const uint32_t span = (uint32_t)S * D * 2;
+            const __amdgpu_buffer_rsrc_t krs = make_rsrc(kh, span), vrs = make_rsrc(vh, span);
+            const uint32_t kA = (uint32_t)(uintptr_t)smem + 2 * w * RC::WAVE, kB = kA + RC::WAVE;
+            u32x4 kra[RC::SEG], vra[RC::SEG], krb[RC::SEG], vrb[RC::SEG];
+            auto fetch2 = [&](int ch, u32x4(&kr)[RC::SEG], u32x4(&vr)[RC::SEG]) {
+#pragma unroll
+                for (int j = 0; j < RC::SEG; ++j) {
+                    const int seg = lane + 64 * j, row = seg / (D / 8), c8 = seg % (D / 8);
+                    const uint32_t off = (uint32_t)((32 * ch + row) * D + 8 * c8) * 2;
+                    kr[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0);
+                    vr[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0);
+                }
+            };
+            auto stage2 = [&](uint32_t kst2, const u32x4(&kr)[RC::SEG], const u32x4(&vr)[RC::SEG]) {
+#pragma unroll
+                for (int j = 0; j < RC::SEG; ++j) {
+                    const int seg = lane + 64 * j, row = seg / (D / 8), c8 = seg % (D / 8);
+                    const uint32_t off = (uint32_t)(row * RC::KP + 8 * c8) * 2;
+                    *reinterpret_cast<NC_LDS(u32x4) *>((uintptr_t)(kst2 + off)) = kr[j];
+                    *reinterpret_cast<NC_LDS(u32x4) *>((uintptr_t)(kst2 + RC::CHUNK + off)) = vr[j];
+                }
+            };
+            auto scores = [&](uint32_t kst2, floatx4(&s)[2]) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    s[t] = floatx4{};
+#pragma unroll
+                    for (int h = 0; h < DH; ++h) {
+                        const int d0 = 32 * h + 8 * g;
+                        half8 kf = half8{};
+                        if (d0 < D)
+                            kf = *reinterpret_cast<const NC_LDS(half8) *>(
+                                (uintptr_t)(kst2 + (uint32_t)((16 * t + c) * RC::KP + d0) * 2));
+                        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[h], s[t], 0, 0, 0);
+                    }
+                }
+            };
+            auto vtread = [&](uint32_t vst2, u32x2(&vt)[2 * DT]) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        const int r = 16 * hf + 4 * g + (c >> 2), d0 = 16 * dt + 4 * (c & 3);
+                        ds_read_tr<0>(vt[2 * dt + hf], vst2 + (uint32_t)(r * RC::KP + d0) * 2);
+                    }
+            };
+            // Online softmax of one chunk into one stream's (m, l, O), returning P (f16).
+            auto softmax = [&](const floatx4(&s)[2], int kt0, float &m, float &lsum, floatx4(&oa)[DT]) {
+                float x[8];
+                float lm = neg_inf();
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int key = kt0 + 16 * (e >> 2) + 4 * g + (e & 3);
+                    x[e] = key > lim_row ? neg_inf() : s[e >> 2][e & 3] * sc;
+                    lm = fmaxf(lm, x[e]);
+                }
+                lm = fmaxf(lm, __shfl_xor(lm, 16));
+                lm = fmaxf(lm, __shfl_xor(lm, 32));
+                const float m_new = fmaxf(m, lm);
+                const float m_use = m_new == neg_inf() ? 0.f : m_new;
+                const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+                lsum *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) oa[dt] *= alpha;
+                m = m_new;
+                half8 pb;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pb[e] = (_Float16)__builtin_amdgcn_exp2f(x[e] - m_use);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const half2v hp = {pb[2 * t], pb[2 * t + 1]};
+                    lsum = __builtin_amdgcn_fdot2(hp, ones, lsum, false);
+                }
+                return pb;
+            };
+            auto pv = [&](const u32x2(&vt)[2 * DT], const half8 &pb, floatx4(&oa)[DT]) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const u32x4 vv = {vt[2 * dt][0], vt[2 * dt][1], vt[2 * dt + 1][0], vt[2 * dt + 1][1]};
+                    oa[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, vv), pb, oa[dt], 0, 0, 0);
+                }
+            };
+            float m1 = neg_inf(), l1 = 0.f;
+            floatx4 o1[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o1[dt] = floatx4{};
+            fetch2(w, kra, vra);
+            fetch2(w + NW, krb, vrb);
+            int ch = w;
+            for (; ch + NW < nch; ch += 2 * NW) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // both regions' previous reads are done
+                stage2(kA, kra, vra);
+                stage2(kB, krb, vrb);
+                asm volatile("" ::: "memory");
+                fetch2(ch + 2 * NW, kra, vra);  // in flight while this pair is computed
+                fetch2(ch + 3 * NW, krb, vrb);
+                floatx4 sa[2], sb[2];
+                scores(kA, sa);
+                scores(kB, sb);
+                u32x2 vta[2 * DT], vtb[2 * DT];
+                vtread(kA + RC::CHUNK, vta);
+                vtread(kB + RC::CHUNK, vtb);
+                const half8 pa = softmax(sa, 32 * ch, mrow, l, oacc);
+                const half8 pbb = softmax(sb, 32 * (ch + NW), m1, l1, o1);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int i = 0; i < 2 * DT; ++i) asm volatile("" : "+v"(vta[i]), "+v"(vtb[i]));
+                pv(vta, pa, oacc);
+                pv(vtb, pbb, o1);
+            }
+            if (ch < nch) {  // an odd last chunk: stream A alone (its registers hold chunk ch)
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                stage2(kA, kra, vra);
+                asm volatile("" ::: "memory");
+                floatx4 sa[2];
+                scores(kA, sa);
+                u32x2 vta[2 * DT];
+                vtread(kA + RC::CHUNK, vta);
+                const half8 pa = softmax(sa, 32 * ch, mrow, l, oacc);
+                wait_lds_tied_any(vta);
+                pv(vta, pa, oacc);
+            }
+            // Stream B into A (row-uniform maxima; a stream that saw no chunk has m = -inf, l = O = 0).
+            const float mm = fmaxf(mrow, m1);
+            const float mu = mm == neg_inf() ? 0.f : mm;
+            const float a0 = __builtin_amdgcn_exp2f(mrow - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+            l = l * a0 + l1 * a1;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) oacc[dt] = oacc[dt] * a0 + o1[dt] * a1;
+            mrow = mm;
+        }
+    }
+
+    for (int ch = w; !pair && ch < nch; ch += NW) {
         const int kt0 = 32 * ch;
         if constexpr (VEC) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous chunk's reads are done
