@@ -68,6 +68,11 @@ struct Variant {
                                        C[0] == 'c', true, Family::kPipe, BF}
 #define GEN(D, C, A, SUF, T, BF) {"nc_flash_fwd_d" #D "_m64_" C SUF T, D, 2, 2, 1, 1, C[0] == 'c', A, \
                                   Family::kGeneric, BF}
+// The generic body in other geometries (32 rows x 8 key splits; 128 rows x 2 key splits).
+#define GENG(D, NQ, NS, C, A, SUF, T, BF) {"nc_flash_fwd_d" #D "_m64_q" #NQ "s" #NS "_" C SUF T, D, NQ, NS, 1, 1, \
+                                           C[0] == 'c', A, Family::kGeneric, BF}
+#define GENG2(D, NQ, NS, T, BF) GENG(D, NQ, NS, "full", true, "", T, BF), GENG(D, NQ, NS, "causal", true, "", T, BF), \
+    GENG(D, NQ, NS, "full", false, "_unaligned", T, BF), GENG(D, NQ, NS, "causal", false, "_unaligned", T, BF)
 // Every kernel of the family, once per element type (T: name suffix, BF: bf16).
 #define VARIANTS(T, BF)                                                                                         \
     PIPE2(64, 8, 1, 2, "full", T, BF), PIPE2(64, 8, 1, 2, "causal", T, BF), PIPE2(64, 4, 1, 2, "full", T, BF),  \
@@ -81,7 +86,8 @@ struct Variant {
     GEN(32, "causal", true, "", T, BF), GEN(64, "full", true, "", T, BF), GEN(64, "causal", true, "", T, BF),   \
     GEN(16, "full", false, "_unaligned", T, BF), GEN(16, "causal", false, "_unaligned", T, BF),                \
     GEN(32, "full", false, "_unaligned", T, BF), GEN(32, "causal", false, "_unaligned", T, BF),                \
-    GEN(64, "full", false, "_unaligned", T, BF), GEN(64, "causal", false, "_unaligned", T, BF), PIPEX(64, T, BF)
+    GEN(64, "full", false, "_unaligned", T, BF), GEN(64, "causal", false, "_unaligned", T, BF), PIPEX(64, T, BF), \
+    GENG2(16, 1, 8, T, BF), GENG2(32, 1, 8, T, BF), GENG2(64, 1, 8, T, BF), GENG2(64, 4, 2, T, BF)
 
 const Variant kVariants[] = {VARIANTS("", false), VARIANTS("_bf16", true)};
 #undef VARIANTS
@@ -89,6 +95,8 @@ const Variant kVariants[] = {VARIANTS("", false), VARIANTS("_bf16", true)};
 #undef PIPE2
 #undef PIPEX
 #undef GEN
+#undef GENG
+#undef GENG2
 
 const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal, bool bf16) {
     for (const auto &v : kVariants)
@@ -111,11 +119,33 @@ uint64_t xsplit_scratch_bytes(uint64_t batch_heads, uint64_t seq_len, uint64_t d
     return NC_XS_COUNTER_BYTES + xsplit_pairs(batch_heads, seq_len) * 2 * (32 * d * 4 + 32 * 8);
 }
 
-const Variant *find_generic(uint32_t d, bool causal, bool aligned, bool bf16) {
+const Variant *find_generic(uint32_t d, uint32_t nq, uint32_t ns, bool causal, bool aligned, bool bf16) {
     for (const auto &v : kVariants)
-        if (v.family == Family::kGeneric && v.d == d && v.causal == causal && v.aligned == aligned && v.bf16 == bf16)
+        if (v.family == Family::kGeneric && v.d == d && v.nq == nq && v.ns == ns && v.causal == causal &&
+            v.aligned == aligned && v.bf16 == bf16)
             return &v;
     return nullptr;
+}
+
+// Geometry of the generic kernels (rows past 16-byte alignment or past 32-bit offsets), from GPU
+// timings of the three on 132 shapes (d 16/32/64, BH 1-128, S 256-8192, causal and not), where
+// these picks come within 0.6 % of the per-shape best on average and the 64-row kernel alone
+// averaged 1.30-1.83x: 32 rows x 8 key splits while the grid is small, 128 x 2 for large d=64
+// grids, the 64-row, 4-wave kernel between.
+const Variant *choose_generic(const nc_flash_options &o, bool aligned) {
+    const uint32_t d = (uint32_t)o.head_dim;
+    const bool causal = o.causal != 0, bf = o.element_type == NC_ELEMENT_BF16;
+    const uint64_t S = o.seq_len, w32 = (S + 31) / 32 * o.batch_heads, w128 = (S + 127) / 128 * o.batch_heads;
+    bool small;
+    if (d == 64) {
+        if (w128 >= (causal ? 384u : 256u)) return find_generic(d, 4, 2, causal, aligned, bf);
+        small = causal ? (w32 <= 384 || (w32 <= 512 && S >= 1024)) : w32 <= 256;
+    } else if (d == 32) {
+        small = w32 <= 768 || (w32 <= 1024 && S >= (causal ? 1024u : 4096u));
+    } else {
+        small = w32 <= 768 || (causal ? (w32 <= 2048 && S >= 1024) : (w32 <= 1024 && S >= 512));
+    }
+    return small ? find_generic(d, 1, 8, causal, aligned, bf) : find_generic(d, 2, 2, causal, aligned, bf);
 }
 
 uint64_t row_stride_of(uint64_t rs, uint64_t d) { return rs == 0 ? d : rs; }
@@ -257,7 +287,7 @@ int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selec
     const bool offsets_fit = max_row < (1ull << 30) && (o.seq_len + 512) * max_row * 2 < (1ull << 31);
     const Variant *v = (aligned && offsets_fit)
                            ? choose_pipe(o)
-                           : find_generic((uint32_t)d, o.causal != 0, aligned, o.element_type == NC_ELEMENT_BF16);
+                           : choose_generic(o, aligned);
     if (!v) return NC_ERROR_NOT_FOUND;
     // Long causal sequences over few heads on the private-staging kernel: pair the light and heavy
     // query blocks so that every workgroup takes about half the heaviest block's keys. It pays once

@@ -1739,6 +1739,17 @@ NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_causal, 32, 2, 2, true, true)
 NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_full, 64, 2, 2, false, true)
 NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_causal, 64, 2, 2, true, true)
 
+// The same body in two more geometries: 32 query rows over 8 key-split waves (small grids: 2-3.5x
+// the 64-row kernels there) and, at d = 64, 128 rows over 2 key splits (large grids: 1.1-1.4x).
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_q1s8_full, 16, 1, 8, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_q1s8_causal, 16, 1, 8, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_q1s8_full, 32, 1, 8, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_q1s8_causal, 32, 1, 8, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_q1s8_full, 64, 1, 8, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_q1s8_causal, 64, 1, 8, true, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_q4s2_full, 64, 4, 2, false, true)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_q4s2_causal, 64, 4, 2, true, true)
+
 // Element-wise variants for slices whose base or strides break 16-byte alignment.
 NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_full_unaligned, 16, 2, 2, false, false)
 NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_causal_unaligned, 16, 2, 2, true, false)
@@ -1746,6 +1757,14 @@ NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_full_unaligned, 32, 2, 2, false, false)
 NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_causal_unaligned, 32, 2, 2, true, false)
 NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_full_unaligned, 64, 2, 2, false, false)
 NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_causal_unaligned, 64, 2, 2, true, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_q1s8_full_unaligned, 16, 1, 8, false, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d16_m64_q1s8_causal_unaligned, 16, 1, 8, true, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_q1s8_full_unaligned, 32, 1, 8, false, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d32_m64_q1s8_causal_unaligned, 32, 1, 8, true, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_q1s8_full_unaligned, 64, 1, 8, false, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_q1s8_causal_unaligned, 64, 1, 8, true, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_q4s2_full_unaligned, 64, 4, 2, false, false)
+NC_FLASH_KERNEL(nc_flash_fwd_d64_m64_q4s2_causal_unaligned, 64, 4, 2, true, false)
 
 // Plain 16-byte copy, used only to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte
 // count (bench.py --calibrate-copy).

@@ -109,7 +109,7 @@ def test_each_bf16_kernel_variant(gpu, name):
     """Every bf16 code-object variant launched directly on a ragged shape (S = 1100)."""
     d = int(re.search(r"_d(\d+)_", name).group(1))
     causal = "_causal" in name
-    m = re.search(r"_q(\d+)s(\d+)p\d+", name)
+    m = re.search(r"_q(\d+)s(\d+)(?:p|_)", name)
     bm, threads = (32 * int(m.group(1)), 64 * int(m.group(1)) * int(m.group(2))) if m else (64, 256)
     s = 1100
     wl = Workload(f"variant_{name}", 2, s, d, causal, 1.0 / math.sqrt(d), (("normal", 0.0, 1.0),) * 3, seed=21,

@@ -215,7 +215,7 @@ def test_each_kernel_variant_parity(gpu, name):
 
     d = int(re.search(r"_d(\d+)_", name).group(1))
     causal = "_causal" in name
-    m = re.search(r"_q(\d+)s(\d+)p\d+(?:t\d+)?_", name)
+    m = re.search(r"_q(\d+)s(\d+)(?:p\d+(?:t\d+)?x?)?_", name)
     bm, threads = (32 * int(m.group(1)), 64 * int(m.group(1)) * int(m.group(2))) if m else (64, 256)
     # S = 1100: every wave of every variant (up to 512 keys per staged block) steps through
     # several blocks, so ring reuse and refills are exercised; S is not a multiple of any tile.
