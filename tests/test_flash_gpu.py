@@ -132,6 +132,17 @@ def test_every_kernel_variant(gpu):
     assert len(seen) >= 6
 
 
+def test_no_kernel_uses_scratch(gpu):
+    """No kernel symbol of the code object (every variant, f16 and bf16) spills registers or keeps
+    an array in private memory: scratch traffic would cost several times the kernel's time."""
+    names = _variant_names()
+    names += [n + "_bf16" for n in names]
+    for name in names:
+        attrs = gpu.get_function(name).attributes()
+        assert attrs.local_size_bytes == 0, f"{name} uses {attrs.local_size_bytes} bytes of scratch"
+    assert len(names) >= 80
+
+
 def test_memset_done_before_stream_work(gpu):
     """nc_memset returns once the fill is complete: a kernel launched right after it on a
     non-blocking stream (which does not wait for the null stream the fill runs on) writes over the
