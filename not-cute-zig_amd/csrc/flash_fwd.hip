@@ -1369,7 +1369,9 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
     const int NW = (int)(blockDim.x >> 6);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-    const int r0 = 16 * (int)blockIdx.x;
+    // Causal: the last (heaviest) query blocks first, so that on grids larger than the machine
+    // holds at once they do not start last.
+    const int r0 = 16 * (int)(causal ? gridDim.x - 1u - blockIdx.x : blockIdx.x);
     const size_t head = blockIdx.y;
     if (r0 >= S) return;
     const uint16_t *qh = q + head * q_stride, *kh = k + head * k_stride, *vh = v + head * v_stride;
