@@ -1,7 +1,9 @@
-"""Seeded random-shape parity sweep on the GPU: batch_heads, seq_len, head_dim, causal, scale
+"""Seeded random-shape parity sweeps on the GPU: batch_heads, seq_len, head_dim, causal, scale
 (including negative and zero), row pitch and slice padding, and misaligned base pointers, so every
 dispatch route (pipelined private/shared staging, generic, element-wise) meets the oracle on shapes
-nobody chose by hand. Rows are checked on a deterministic subset for the longer sequences."""
+nobody chose by hand; a second sweep takes many heads over short and mid sequences in f16 and bf16,
+where the dispatch picks the four- and eight-query-wave kernels. Rows are checked on a
+deterministic subset for the longer sequences."""
 
 import math
 
@@ -68,3 +70,38 @@ def test_sweep_reaches_every_route():
         fams.add("unaligned" if offset or n.endswith("unaligned") else "m64" if "_m64_" in n else
                  "private" if "_q1s" in n else "shared")
     assert {"private", "shared", "unaligned"} <= fams, names
+
+
+N_WIDE = 48
+
+
+def random_wide_case(i: int):
+    """Many heads over short and mid sequences (the grids where the dispatch prices the four- and
+    eight-query-wave kernels), f16 and bf16 alternately, dense or row-padded layouts."""
+    rng = np.random.default_rng(5000 + i)
+    d = int(rng.choice([16, 32, 64]))
+    bh = int(rng.integers(64, 513))
+    s = int(rng.integers(40, 700))
+    causal = bool(rng.integers(0, 2))
+    dtype = "bf16" if i % 2 else "f16"
+    rows = {}
+    if rng.integers(0, 2):
+        rows = dict(q_row=d + 8, k_row=d, v_row=d + 16, o_row=d + 4)
+    wl = Workload(f"wide{i}_bh{bh}_s{s}_d{d}_{'c' if causal else 'n'}_{dtype}", bh, s, d, causal, 1.0 / math.sqrt(d),
+                  (("normal", 0.0, 1.0),) * 3, seed=6000 + i, dtype=dtype, **rows)
+    return wl
+
+
+@pytest.mark.parametrize("i", range(N_WIDE))
+def test_random_wide_shape(gpu, i):
+    wl = random_wide_case(i)
+    sel = nc.select_kernel(wl.options())
+    rows = sample_rows(wl.seq_len, extra=8, seed=i)
+    print(f"[case] {wl.describe()} rows={len(rows)} -> {sel.name.decode()}", flush=True)
+    q, k, v = wl.make_inputs()
+    o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
+    ref = fc.oracle(wl, q, k, v, rows=rows, o_init=o_init)
+    out = fc.run_gpu(gpu, wl, q, k, v, o_init)
+    max_abs, max_rel = fc.parity_bar(wl.dtype)
+    fc.assert_parity(out, ref, fc.active_index(wl, rows), wl.name, max_abs=max_abs, max_rel=max_rel)
+    fc.assert_pads_untouched(out, o_init, wl, wl.name)
