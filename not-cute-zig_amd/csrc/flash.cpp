@@ -214,8 +214,11 @@ double pipe_cost(const PipeModel &m, const Variant &v, uint64_t batch_heads, uin
     auto job = [&](uint64_t i) { return (double)pipe_steps(v, S, true, nqb - 1 - (256 * i) / batch_heads) + m.rho; };
     double t = 0.0;
     if (ncu > 512) {  // the CU stays full but for a short tail: its 1/256 share of all the work
-        for (uint64_t qb = 0; qb < nqb; ++qb) t += (double)pipe_steps(v, S, true, qb);
-        t = t * (double)batch_heads / 256.0 + (double)ncu * m.rho;
+        // (over at most 4096 query blocks, evenly strided: steps grow linearly with the block)
+        const uint64_t stride = nqb > 4096 ? (nqb + 4095) / 4096 : 1;
+        uint64_t counted = 0;
+        for (uint64_t qb = 0; qb < nqb; qb += stride, ++counted) t += (double)pipe_steps(v, S, true, qb);
+        t = t * (double)nqb / (double)counted * (double)batch_heads / 256.0 + (double)ncu * m.rho;
         return m.a + t * per(m.wg_per_cu) / m.wg_per_cu;
     }
     double act[8];
