@@ -167,8 +167,9 @@ const char *reference_kernel(const nc_flash_options &o) {
 }
 
 // MI355X dispatch (256 CUs): at d = 64 and 32 every pipelined kernel of the head size is priced by a
-// cost model and the cheapest is launched (d = 16: fitted thresholds, in choose_pipe). A kernel's workgroups are dealt to the CUs in block order (heaviest
-// causal query blocks first), so the busiest CU holds workgroups 0, 256, 512, ... . It runs up to
+// cost model and the cheapest is launched (d = 16: fitted thresholds, in choose_pipe). A kernel's
+// workgroups are dealt to the CUs in block order (heaviest causal query blocks first), so the
+// busiest CU holds workgroups 0, 256, 512, ... . It runs up to
 // wg_per_cu of them at once (from each kernel's registers and LDS); each resident workgroup needs
 // rho + steps units of work, steps being its busiest wave's sequential 32-key tiles (the padded key
 // blocks up to its last visible key), and advances one unit per max(lat, k * waves_per_simd * tau)
