@@ -250,8 +250,10 @@ const Variant *choose_pipe(const nc_flash_options &o) {
         // its workgroups, more for longer sequences, then q2s4 from 192-768 of its own.
         const uint64_t S = o.seq_len, bh = o.batch_heads;
         const uint64_t w128 = (S + 127) / 128 * bh, w64 = (S + 63) / 64 * bh;
-        if (w128 >= (S <= 512 ? 384u : S <= (causal ? 2048u : 1024u) ? 768u : 1536u)) return find_pipe(d, 4, 1, causal, bf);
-        if (w64 >= (S <= (causal ? 512u : 256u) ? 192u : S <= 1024 ? 384u : 768u)) return find_pipe(d, 2, 4, causal, bf);
+        const uint64_t need4 = S <= 512 ? 384u : S <= (causal ? 2048u : 1024u) ? 768u : 1536u;
+        const uint64_t need2 = S <= (causal ? 512u : 256u) ? 192u : S <= 1024 ? 384u : 768u;
+        if (w128 >= need4) return find_pipe(d, 4, 1, causal, bf);
+        if (w64 >= need2) return find_pipe(d, 2, 4, causal, bf);
         return find_pipe(d, 1, 8, causal, bf);
     }
     const Variant *best = nullptr;
