@@ -87,7 +87,9 @@ struct Variant {
     GEN(16, "full", false, "_unaligned", T, BF), GEN(16, "causal", false, "_unaligned", T, BF),                \
     GEN(32, "full", false, "_unaligned", T, BF), GEN(32, "causal", false, "_unaligned", T, BF),                \
     GEN(64, "full", false, "_unaligned", T, BF), GEN(64, "causal", false, "_unaligned", T, BF), PIPEX(64, T, BF), \
-    GENG2(16, 1, 8, T, BF), GENG2(32, 1, 8, T, BF), GENG2(64, 1, 8, T, BF), GENG2(64, 4, 2, T, BF)
+    GENG2(16, 1, 8, T, BF), GENG2(32, 1, 8, T, BF), GENG2(64, 1, 8, T, BF), GENG2(64, 4, 2, T, BF),          \
+    PIPE(64, 1, 8, 1, "full", T, BF), PIPE(64, 1, 8, 1, "causal", T, BF), PIPE(32, 1, 8, 1, "full", T, BF),   \
+    PIPE(32, 1, 8, 1, "causal", T, BF), PIPE(16, 1, 8, 1, "full", T, BF), PIPE(16, 1, 8, 1, "causal", T, BF)
 
 const Variant kVariants[] = {VARIANTS("", false), VARIANTS("_bf16", true)};
 #undef VARIANTS
@@ -102,6 +104,15 @@ const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal, bool
     for (const auto &v : kVariants)
         if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.causal == causal && v.bf16 == bf16 &&
             !v.xsplit)
+            return &v;
+    return nullptr;
+}
+
+// The same, with a given ring depth (find_pipe returns the first in the table: the two-stage one).
+const Variant *find_pipe_stages(uint32_t d, uint32_t nq, uint32_t ns, uint32_t nstage, bool causal, bool bf16) {
+    for (const auto &v : kVariants)
+        if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.nstage == nstage &&
+            v.causal == causal && v.bf16 == bf16 && !v.xsplit)
             return &v;
     return nullptr;
 }
@@ -239,7 +250,23 @@ double pipe_cost(const PipeModel &m, const Variant &v, uint64_t batch_heads, uin
     return m.a + t;
 }
 
+const Variant *choose_pipe_layout(const nc_flash_options &o);
+
+// Private staging (one query wave) with one ring stage on short sequences: with at most three
+// 32-key tiles per wave, the second stage's prologue costs more than it hides. Measured against the
+// two-stage kernels on 40 shapes (d 32/64, BH 1-32, S 128-2048): 2-10 % faster up to S = 768 (d=64
+// non-causal: 512), 1-6 % slower from S = 1024.
 const Variant *choose_pipe(const nc_flash_options &o) {
+    const Variant *v = choose_pipe_layout(o);
+    const bool causal = o.causal != 0;
+    if (v && v->nq == 1 && o.seq_len <= (v->d == 64 && !causal ? 512u : 768u)) {
+        const Variant *p1 = find_pipe_stages(v->d, 1, v->ns, 1, causal, v->bf16);
+        if (p1) v = p1;
+    }
+    return v;
+}
+
+const Variant *choose_pipe_layout(const nc_flash_options &o) {
     const uint32_t d = (uint32_t)o.head_dim;
     const bool causal = o.causal != 0;
     const bool bf = o.element_type == NC_ELEMENT_BF16;

@@ -1859,6 +1859,13 @@ NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_full, 16, 2, 4, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q2s4p2_causal, 16, 2, 4, true, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_full, 16, 1, 8, false, 2, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p2_causal, 16, 1, 8, true, 2, 1)
+// Private staging with one ring stage, for short sequences (at most three 32-key tiles per wave).
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p1_full, 64, 1, 8, false, 1, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p1_causal, 64, 1, 8, true, 1, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p1_full, 32, 1, 8, false, 1, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p1_causal, 32, 1, 8, true, 1, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p1_full, 16, 1, 8, false, 1, 1)
+NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p1_causal, 16, 1, 8, true, 1, 1)
 
 // Reference-ABI symbols (src/flash_v2.zig:23, src/flash_opt.zig:17, src/flash_h64.zig:21,
 // src/flash_h64_bn32.zig:26, src/flash_h64_causal.zig:20, src/kernels.zig:380): one body, launched
