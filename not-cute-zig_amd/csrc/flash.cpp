@@ -254,7 +254,7 @@ const Variant *choose_pipe_layout(const nc_flash_options &o);
 
 // Private staging (one query wave) with one ring stage on short sequences: with at most three
 // 32-key tiles per wave, the second stage's prologue costs more than it hides. Measured against the
-// two-stage kernels on 40 shapes (d 32/64, BH 1-32, S 128-2048): 2-10 % faster up to S = 768 (d=64
+// two-stage kernels on 58 shapes (d 16/32/64, BH 1-32, S 32-2048): 2-10 % faster up to S = 768 (d=64
 // non-causal: 512), 1-6 % slower from S = 1024.
 const Variant *choose_pipe(const nc_flash_options &o) {
     const Variant *v = choose_pipe_layout(o);
