@@ -356,6 +356,17 @@ def test_dispatch_picks_measured_winner(case, kernel):
         assert f"_{kernel}_" in name.decode(), (case, dtype, name)
 
 
+@pytest.mark.parametrize("d,causal,s_last", [(64, True, 768), (64, False, 512), (32, True, 768), (32, False, 768),
+                                             (16, True, 768), (16, False, 768)])
+def test_one_stage_private_kernel_boundary(d, causal, s_last):
+    """Short sequences on the private-staging route take the one-stage kernel (at most three 32-key
+    tiles per wave), longer ones the two-stage kernel; both element types."""
+    for dtype in ("f16", "bf16"):
+        for s, stages in ((s_last, "p1"), (s_last + 1, "p2")):
+            name = nc.select_kernel(nc.options(batch_heads=2, seq_len=s, head_dim=d, causal=causal, dtype=dtype)).name
+            assert f"_q1s8{stages}_" in name.decode(), (d, causal, s, dtype, name)
+
+
 def test_pair_split_dispatch_region():
     """The pair-split kernel replaces the private-staging one for d=64 causal shapes with at least 96
     query blocks whose grid fits one workgroup per CU (measured faster there, slower elsewhere)."""
