@@ -255,11 +255,18 @@ const Variant *choose_pipe_layout(const nc_flash_options &o);
 // Private staging (one query wave) with one ring stage on short sequences: with at most three
 // 32-key tiles per wave, the second stage's prologue costs more than it hides. Measured against the
 // two-stage kernels on 58 shapes (d 16/32/64, BH 1-32, S 32-2048): 2-10 % faster up to S = 768 (d=64
-// non-causal: 512), 1-6 % slower from S = 1024.
+// non-causal: 512), 1-6 % slower from S = 1024 on those grids of at most 256 workgroups.
 const Variant *choose_pipe(const nc_flash_options &o) {
     const Variant *v = choose_pipe_layout(o);
     const bool causal = o.causal != 0;
-    if (v && v->nq == 1 && o.seq_len <= (v->d == 64 && !causal ? 512u : 768u)) {
+    // At d = 64 it is also faster wherever a CU runs several of the workgroups, up to 4096 of them
+    // (S > 768, mean of p1/p2 over 311 shapes: causal 513-4096 workgroups 0.89-0.92x, worst 1.04x;
+    // non-causal 257-4096 0.91-0.96x, worst 1.03x). It is slower in one round (up to 256: 1.04x)
+    // and on large causal grids (over 4096: up to 1.63x); at d = 32 and 16 the two are within 2 %.
+    const uint64_t wg32 = (o.seq_len + 31) / 32 * o.batch_heads;
+    const bool shared_cu = wg32 >= (causal ? 513u : 257u) && wg32 <= 4096u;
+    const bool short_seq = o.seq_len <= (v && v->d == 64 && !causal ? 512u : 768u);
+    if (v && v->nq == 1 && (short_seq || (v->d == 64 && shared_cu))) {
         const Variant *p1 = find_pipe_stages(v->d, 1, v->ns, 1, causal, v->bf16);
         if (p1) v = p1;
     }

@@ -341,6 +341,8 @@ MEASURED_WINNERS = [
     ((64, 4, 2351, True), "q1s8p2"),  # 9.5 us, next 1.63x
     ((64, 6, 2048, True), "q1s8p2"),  # 10.9 us, q2s4 1.27x (one-stage q1s8 ties)
     ((64, 4, 4096, True), "q1s8p2"),  # 19.3 us, q2s4 1.25x (one-stage q1s8 ties)
+    ((64, 3, 6000, True), "q1s8p1"),  # 28.4 us, two-stage 1.06x, q2s4 1.23x
+    ((64, 2, 12000, True), "q1s8p1"),  # 56.9 us, two-stage 1.09x
     ((64, 48, 384, True), "q2s4p2"),  # 6.3 us, next 1.44x
     ((64, 24, 1536, True), "q2s4p2"),  # 15.8 us, next 1.40x
     ((64, 776, 91, True), "q4s1p2t2"),  # 9.0 us, next 1.68x
