@@ -11,9 +11,10 @@ not time a GPU that is still raising its clock.
 
 Prints ONE JSON line (rank 0, N=1) with the metric of the benchmark plan, a `roofline` object for
 the flash kernel, a `cpu_baseline` object (the CPU oracle, a port of the reference's scalar CPU
-reference, timed on this host on the same workload) and `extra_workloads`: the long-sequence
-configurations c4 and c5 timed the same way, each with its own parity check, and `mfma_ceiling`: the
-f16 MFMA rate the chip sustains on operands drawn like the inputs (nc_util_mfma_ceiling).
+reference, timed on this host on the same workload) and `extra_workloads`: the other configurations
+timed the same way, each with its own parity check (c1 and c2, latency/HBM-bound, also as GB/s against
+the 8 TB/s HBM peak; c4 and c5, MFMA-bound), and `mfma_ceiling`: the f16 MFMA rate the chip sustains
+on operands drawn like the inputs (nc_util_mfma_ceiling).
 """
 
 from __future__ import annotations
@@ -218,8 +219,9 @@ def measure_mfma_ceiling(mod, stream, budget_ms: float, ops16) -> dict:
 
 
 def measure_extra(mod, name: str, args) -> dict:
-    """One more workload (c4 / c5: the MFMA-bound configurations) timed exactly like the headline,
-    with its own parity check on sampled query rows. Reported as extra keys of the one JSON line."""
+    """One more workload timed exactly like the headline, with its own parity check (every query row
+    up to S=1024, else sampled rows). Reported as extra keys of the one JSON line, with TFLOP/s and,
+    for every workload, the algorithmic HBM rate (bytes of Q/K/V read once and O written once)."""
     wl = CONFIGS[name]
     if args.dtype != wl.dtype:
         wl = dataclasses.replace(wl, dtype=args.dtype)
@@ -238,10 +240,10 @@ def measure_extra(mod, name: str, args) -> dict:
         launch()
         stream.synchronize()
         max_abs = None
+        rows = None if wl.seq_len <= 1024 else np.arange(0, wl.seq_len, 97)
         if not args.no_verify:
             import flashcheck  # noqa: E402  (checker only)
 
-            rows = np.arange(0, wl.seq_len, 97)
             ref = flashcheck.oracle(wl, q, k, v, rows=rows)
             max_abs, max_rel = flashcheck.errors(do.download(np.float32, wl.length("o")), ref,
                                                  flashcheck.active_index(wl, rows))
@@ -250,15 +252,21 @@ def measure_extra(mod, name: str, args) -> dict:
                 raise RuntimeError(f"{name}: parity failure max-abs {max_abs} max-rel {max_rel}")
         t = time_graph(stream, launch, args.steps, args.warmup, args.graph_batch, args.settle_ms)
         tflops = work["flops"] / (t["ms_per_step"] * 1e-3) / 1e12
+        gbps = work["bytes"] / (t["ms_per_step"] * 1e-3) / 1e9
         log(f"bench: {wl.describe()} -> {sel.name.decode()}: {t['ms_per_step'] * 1e3:.2f} us/step, "
-            f"{tflops:.1f} TFLOP/s ({100 * tflops / PEAK_F16_TFLOPS:.2f} % of f16 peak), parity max-abs {max_abs}")
+            f"{tflops:.1f} TFLOP/s ({100 * tflops / PEAK_F16_TFLOPS:.2f} % of f16 peak), {gbps:.1f} GB/s, "
+            f"parity max-abs {max_abs}")
         return {"workload": f"{wl.name}: BH={wl.batch_heads} S={wl.seq_len} d={wl.head_dim} "
                             f"{'causal' if wl.causal else 'non-causal'}, Q/K/V {wl.dtype} {describe_dists(wl.dists)} "
                             f"seed {wl.seed}, scale {wl.scale:g}",
                 "kernel": sel.name.decode(), "ms_per_step": round(t["ms_per_step"], 6), "steps": t["steps"],
                 "settle_ms": t["settle_ms"], "tflops": round(tflops, 2),
                 "pct_f16_mfma_peak": round(100.0 * tflops / PEAK_F16_TFLOPS, 3), "flops_per_step": work["flops"],
-                "parity_max_abs": max_abs, "parity_rows": "every 97th query row of every slice"}
+                "bound": "hbm" if work["flops"] / work["bytes"] * PEAK_HBM_GBPS / 1e3 < PEAK_F16_TFLOPS else "mfma",
+                "bytes_per_step": work["bytes"], "gbps": round(gbps, 2),
+                "pct_hbm_peak": round(100.0 * gbps / PEAK_HBM_GBPS, 4),
+                "parity_max_abs": max_abs,
+                "parity_rows": "every query row" if rows is None else "every 97th query row of every slice"}
     finally:
         for b in (dq, dk, dv, do):
             b.free()
@@ -275,7 +283,7 @@ def main() -> int:
     ap.add_argument("--graph-batch", type=int, default=100, help="launches captured per HIP graph")
     ap.add_argument("--settle-ms", type=float, default=300.0,
                     help="untimed clock-settle replays of the timed graph, in wall-clock ms, after --warmup")
-    ap.add_argument("--extra", default="c4,c5",
+    ap.add_argument("--extra", default="c1,c2_causal,c2_full,c4,c5",
                     help="comma-separated extra workloads timed the same way (extra keys of the JSON line; '' for none)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget (0: skip)")
     ap.add_argument("--mfma-ceiling-ms", type=float, default=1000.0,
@@ -408,7 +416,8 @@ def main() -> int:
     if args.mfma_ceiling_ms > 0:
         ceiling = measure_mfma_ceiling(mod, stream, args.mfma_ceiling_ms, nc.fill_normal(1 << 20, 7, 0, 0.0, 1.0))
         for x in extra.values():
-            x["pct_of_mfma_ceiling"] = round(100.0 * x["tflops"] / ceiling["tflops"], 2)
+            if x["bound"] == "mfma":
+                x["pct_of_mfma_ceiling"] = round(100.0 * x["tflops"] / ceiling["tflops"], 2)
 
     cpu = cpu_all = None
     if args.cpu_seconds > 0:

@@ -14,10 +14,10 @@
  *   - Device buffers are plain pointers plus element counts; no C++ or torch types cross the ABI.
  *   - Q/K/V are IEEE binary16 stored as uint16_t bit patterns, O is float32.
  *   - Like the reference, launches are asynchronous; results become visible after a synchronising
- *     copy or an nc_stream_synchronize / nc_device_synchronize. A launch allocates nothing, except
- *     that the first launch on a module whose kernel needs scratch memory (the pair-split kernels:
- *     selection.scratch_bytes > 0) allocates the module's workspace, kept until nc_module_unload;
- *     nc_flash_reserve_workspace allocates it ahead of time (e.g. before a graph capture).
+ *     copy or an nc_stream_synchronize / nc_device_synchronize. A launch allocates nothing and does
+ *     not synchronise: the kernels that need scratch memory (the pair-split kernels,
+ *     selection.scratch_bytes > 0) use a static device buffer compiled into this library, one per
+ *     GPU, which nc_init sets up on every visible GPU.
  *   - One process, one GPU (device 0), one calling thread, as in the reference.
  *
  * The same header is included by the device code (flash_fwd.hip) for the kernel argument block.
@@ -72,7 +72,9 @@ typedef struct nc_function_st *nc_function; /* CUfunction -> hipFunction_t */
 typedef void *nc_stream;                    /* CUstream   -> hipStream_t, NULL = default stream */
 typedef void *nc_event;                     /* CUevent    -> hipEvent_t */
 
-/* cuda.init (src/cuda.zig:181-196): select device 0. NC_ERROR_NO_DEVICE without a GPU. Idempotent. */
+/* cuda.init (src/cuda.zig:181-196): select device 0. NC_ERROR_NO_DEVICE without a GPU. Idempotent.
+ * Also sets up the pair-split kernels' static scratch on every visible GPU (its address, and its
+ * exchange counters zeroed; zeroed again by an nc_init that follows nc_deinit). */
 int nc_init(void);
 /* cuda.deinit (src/cuda.zig:198-204). */
 void nc_deinit(void);
@@ -284,7 +286,9 @@ typedef struct nc_flash_kernel_args {
 
 /* Scratch bytes the kernel `name` needs for a launch with these options (0 for every kernel but the
  * pair-split ones), for callers that launch a kernel by name with their own scratch buffer, which
- * must be zeroed before its first use. NC_ERROR_NOT_FOUND for a name that is not a flash kernel. */
+ * must be zeroed before its first use. NC_ERROR_NOT_FOUND for a name that is not a flash kernel;
+ * NC_ERROR_INVALID_VALUE for a pair-split launch with more than NC_XS_MAX_PAIRS pairs (such a
+ * by-name launch writes nothing). */
 int nc_flash_kernel_scratch_bytes(const char *name, const nc_flash_options *opts, uint64_t *bytes);
 
 /* Fill the argument block for `sel` (row strides resolved, num_q_blocks derived). */
@@ -294,34 +298,45 @@ int nc_flash_pack_args(const nc_flash_options *opts, const nc_flash_kernel_selec
 
 /* flash.launch (src/flash.zig:31-70) + requireLen (src/flash.zig:98-100): validate, require
  * q_len >= batch_heads*q_stride (and likewise k, v, o; lengths in elements), select, look the
- * kernel up in `module`, launch on the default stream. Asynchronous; allocates nothing. */
+ * kernel up in `module`, launch on the default stream. Asynchronous; allocates nothing and does not
+ * synchronise (so it may be captured into a HIP graph, first launch included). */
 int nc_flash_launch(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
                     const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts);
 /* Same on an explicit stream (a strict superset: the reference always uses the null stream).
- * Launches whose kernel uses the module's workspace (selection.scratch_bytes > 0) must not overlap
- * in time with another such launch on the same module (e.g. on two streams): they share it. */
+ * Launches whose kernel uses scratch (selection.scratch_bytes > 0) must not overlap in time with
+ * another such launch on the same GPU (e.g. on two streams): they share the GPU's static scratch
+ * (with nc_flash_launch_noalloc). */
 int nc_flash_launch_async(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k,
                           size_t k_len, const uint16_t *v, size_t v_len, float *o, size_t o_len,
                           const nc_flash_options *opts, nc_stream stream);
 
 /* No counterpart in the reference (whose kernels use no scratch memory): for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). The same launch as nc_flash_launch_async, except that a kernel needing scratch gets a
- * static device buffer of NC_NOALLOC_SCRATCH_BYTES compiled into this library (one per GPU, held
- * until the process ends) instead of the module's workspace; it never allocates or frees anything.
- * NC_ERROR_INVALID_VALUE when the selected kernel would need more scratch than that. Every call on
- * one GPU shares the buffer: calls that overlap in time on one GPU (e.g. on two streams) race. */
+ * hipMalloc). The same launch as nc_flash_launch_async, with the contract stated: a kernel needing
+ * scratch gets the static device buffer of NC_NOALLOC_SCRATCH_BYTES compiled into this library (one
+ * per GPU, held until the process ends); it never allocates or frees anything, and returns
+ * NC_ERROR_INVALID_VALUE when the selected kernel would need more scratch than that. Every
+ * pair-split launch on one GPU shares the buffer: launches that overlap in time on one GPU (e.g. on
+ * two streams) race. */
 #define NC_NOALLOC_SCRATCH_BYTES (4u << 20)
 int nc_flash_launch_noalloc(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k,
                             size_t k_len, const uint16_t *v, size_t v_len, float *o, size_t o_len,
                             const nc_flash_options *opts, nc_stream stream);
 
-/* Extension (no counterpart in the reference, whose kernels use no scratch memory): make the
- * module's workspace large enough for a launch with these options, allocating it now (device memory,
- * zeroed), so that later launches allocate nothing. Stores the workspace in *workspace (may be NULL)
- * for callers that launch the selected kernel themselves: they put it in nc_flash_kernel_args.scratch.
- * Stores NULL, allocating nothing, when the selected kernel needs no scratch. */
+/* Extension (no counterpart in the reference, whose kernels use no scratch memory), for callers that
+ * launch the selected kernel by name themselves: make the module's workspace large enough for a
+ * launch with these options (allocating and zeroing device memory when it must grow) and store it in
+ * *workspace (may be NULL); they put it in nc_flash_kernel_args.scratch. Stores NULL, allocating
+ * nothing, when the selected kernel needs no scratch. A returned workspace stays valid until
+ * nc_module_unload: growing it allocates a new one and keeps the old. nc_flash_launch does not use it. */
 int nc_flash_reserve_workspace(nc_module module, const nc_flash_options *opts, void **workspace);
+
+/* Extension (no counterpart in the reference): zero the pair-split exchange counters again, in the
+ * current GPU's static scratch and in `module`'s workspaces (module may be NULL), then synchronise the
+ * device. The counters are even between launches; a launch that overlapped another pair-split
+ * launch on the same GPU, or one that was aborted, can leave them odd, which breaks later pair-split
+ * results until this is called. Call it with no launch in flight and outside a stream capture. */
+int nc_flash_reset_scratch(nc_module module);
 
 /* Work model of one launch: flops and bytes as the reference's harness counts them
  * (src/main.zig:843-845, 1032-1034: causal keys = S(S+1)/2), and the half-square causal count

@@ -13,14 +13,18 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdint>
 #include <cstring>
 #include <limits>
 
 #include "notcute_flash.h"
 
-// hip_api.cpp: the module's workspace, grown (and zeroed) on demand.
+// hip_api.cpp: the module's workspace for by-name callers, grown (and zeroed) on demand; error text.
 extern "C" int nc_internal_module_workspace(nc_module module, size_t bytes, void **out);
+extern "C" int nc_internal_fail(int status, const char *what);
+// noalloc.hip: the current device's static scratch of the pair-split kernels, and its size.
+extern "C" int nc_internal_static_scratch(void **out, size_t *cap);
 
 namespace {
 
@@ -448,8 +452,10 @@ int nc_flash_pack_args(const nc_flash_options *opts, const nc_flash_kernel_selec
 
 namespace {
 
-// flash.launch for both entry points: the scratch of a kernel that needs one comes from the module's
-// workspace (scratch == nullptr) or from the caller's buffer of scratch_cap bytes.
+// flash.launch for every entry point: the scratch of a kernel that needs one (the pair-split
+// kernels) is the caller's buffer of scratch_cap bytes, or with scratch == nullptr the library's
+// static scratch on the current device (set up by nc_init), so a launch allocates nothing and does
+// not synchronise (src/flash.zig:31-70).
 int flash_launch_impl(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
                       const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts,
                       nc_stream stream, void *scratch, size_t scratch_cap) {
@@ -473,13 +479,17 @@ int flash_launch_impl(nc_module module, const uint16_t *q, size_t q_len, const u
     st = nc_flash_pack_args(opts, &sel, q, k, v, o, &args);
     if (st) return st;
     if (sel.scratch_bytes) {
-        if (scratch) {
-            if (sel.scratch_bytes > scratch_cap) return NC_ERROR_INVALID_VALUE;
-            args.scratch = scratch;
-        } else {
-            st = nc_internal_module_workspace(module, sel.scratch_bytes, &args.scratch);
+        if (!scratch) {
+            st = nc_internal_static_scratch(&scratch, &scratch_cap);
             if (st) return st;
         }
+        if (sel.scratch_bytes > scratch_cap) {
+            char msg[200];
+            std::snprintf(msg, sizeof msg, "flash launch: %s needs %llu bytes of scratch, more than the %llu available",
+                          sel.name, (unsigned long long)sel.scratch_bytes, (unsigned long long)scratch_cap);
+            return nc_internal_fail(NC_ERROR_INVALID_VALUE, msg);
+        }
+        args.scratch = scratch;
     }
     nc_launch_config cfg;
     std::memset(&cfg, 0, sizeof cfg);
@@ -524,7 +534,13 @@ int nc_flash_kernel_scratch_bytes(const char *name, const nc_flash_options *opts
     *bytes = 0;
     for (const auto &v : kVariants)
         if (std::strcmp(v.name, name) == 0) {
-            if (v.xsplit) *bytes = xsplit_scratch_bytes(opts->batch_heads, opts->seq_len, v.d);
+            if (v.xsplit) {
+                // one exchange counter per pair, and the counter region holds NC_XS_MAX_PAIRS
+                if (xsplit_pairs(opts->batch_heads, opts->seq_len) > NC_XS_MAX_PAIRS)
+                    return nc_internal_fail(NC_ERROR_INVALID_VALUE,
+                                            "nc_flash_kernel_scratch_bytes: more pairs than NC_XS_MAX_PAIRS");
+                *bytes = xsplit_scratch_bytes(opts->batch_heads, opts->seq_len, v.d);
+            }
             return NC_SUCCESS;
         }
     return NC_ERROR_NOT_FOUND;

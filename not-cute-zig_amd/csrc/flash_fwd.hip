@@ -489,11 +489,6 @@ struct Swz {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
-// The same descriptor as four words, for buffer instructions issued through asm.
-__device__ __forceinline__ u32x4 rsrc_words(const void *base, uint32_t bytes) {
-    const uint64_t p = (uint64_t)(uintptr_t)base;
-    return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
-}
 
 // s_waitcnt vmcnt(n) with lgkmcnt(0), then a plain workgroup barrier (no memory fence, so loads of
 // later blocks stay in flight). The asm memory clobber keeps the compiler from moving LDS accesses
@@ -514,8 +509,9 @@ __device__ __forceinline__ void wait_vm_only() {
     asm volatile("" ::: "memory");
 }
 
-// An empty asm statement that consumes the K fragments: every compiler-issued K read has then
-// been waited for, so asm-issued LDS reads that follow never sit under a compiler lgkmcnt wait.
+// An empty asm statement that consumes the K fragments. It only orders the schedule: the V^T reads
+// of a tile are issued after its K reads have landed, so their latency hides behind the softmax
+// rather than in front of the S^T products.
 template <int N>
 __device__ __forceinline__ void lds_reads_done(half8 (&k)[N]) {
 #pragma unroll
@@ -526,17 +522,6 @@ __device__ __forceinline__ void lds_reads_done(half8 (&k)[N]) {
             asm volatile("" ::"v"(k[i]), "v"(k[i + 1]), "v"(k[i + 2]), "v"(k[i + 3]));
         }
     }
-}
-
-// s_waitcnt lgkmcnt(0) that the compiler sees as producing the given registers, so no consumer of
-// an asm-issued LDS read can be scheduled before the wait. Registers beyond the first four are
-// tied by empty asm statements that follow the wait (asm volatile statements keep their order).
-template <int N>
-__device__ __forceinline__ void wait_lds_tied(u32x2 (&v)[N]) {
-    static_assert(N % 4 == 0, "groups of four");
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
-#pragma unroll
-    for (int i = 4; i < N; i += 4) asm volatile("" : "+v"(v[i]), "+v"(v[i + 1]), "+v"(v[i + 2]), "+v"(v[i + 3]));
 }
 
 template <int N>
@@ -579,16 +564,13 @@ __device__ __forceinline__ void wait_block(int ahead) {
     with_clamped<0, MAXA>(ahead, [](auto ac) { wait_vm_barrier<decltype(ac)::value * LPW>(); });
 }
 
-// 16-byte buffer load into registers through asm. The compiler does not track it, so it never
-// places a vmcnt wait of its own for the result; the caller waits with s_waitcnt and then ties
-// the registers to that wait (tie_regs). (A compiler-tracked load of loop-invariant registers
-// made the compiler wait, inside the loop, on every vm operation issued before the first use,
-// including the prefetch issued a few instructions earlier.)
-__device__ __forceinline__ void buffer_load_b128_asm(half8 &dst, u32x4 rsrc, uint32_t voff) {
-    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(dst) : "v"(voff), "s"(rsrc));
-}
+// Every load that writes registers is issued by the compiler, which places its own waits before
+// the first use of each result (no asm-issued load leaves the compiler holding a register whose
+// data may not have landed). use_now() is an early use of loop-invariant registers: it puts the
+// compiler's wait for them at that point, after the prologue, instead of inside the key loop at
+// their first real use, where it would also wait on the K/V prefetch issued just before.
 template <int N>
-__device__ __forceinline__ void tie_regs(half8 (&r)[N]) {
+__device__ __forceinline__ void use_now(half8 (&r)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) asm volatile("" : "+v"(r[i]));
 }
@@ -599,12 +581,18 @@ template <int OFF>
 __device__ __forceinline__ half8 lds_load_b128(uint32_t addr) {
     return *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(addr + (uint32_t)OFF));
 }
+// ds_read_b64_tr_b16 through the gfx950 builtin, so the compiler tracks the result like any load.
+// The pointer reaches the builtin as a restrict parameter: the scope metadata this leaves on the
+// read tells the compiler's wait placement that it does not alias the buffer->LDS loads in flight,
+// so it is not made to wait (vmcnt(0)) for the prefetch of later blocks, exactly as for the K
+// reads above. The kernels order every read after the staged block it reads by their own waits.
+typedef short short4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 read_tr_b64(const NC_LDS(short4v) *__restrict__ p) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<NC_LDS(short4v) *>(p)));
+}
 template <int OFF>
 __device__ __forceinline__ void ds_read_tr(u32x2 &out, uint32_t addr) {
-    if constexpr (OFF < 65536)
-        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(out) : "v"(addr), "i"(OFF));
-    else
-        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(out) : "v"(addr + (uint32_t)OFF));
+    out = read_tr_b64(reinterpret_cast<const NC_LDS(short4v) *>((uintptr_t)(addr + (uint32_t)OFF)));
 }
 
 template <int D, int NQ, int NS, int NSTAGE, int SUB>
@@ -692,6 +680,10 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     const int S = (int)a.seq_len;
     const uint32_t bh = a.batch_heads;
     const uint32_t nqb = a.num_q_blocks;
+    // More pairs than the counter region holds would put counters inside the partial slots; the
+    // host API refuses such shapes (nc_flash_kernel_scratch_bytes), and a by-name launch of one
+    // writes nothing.
+    if (XS && (uint64_t)bh * (nqb >> 1) > NC_XS_MAX_PAIRS) return;
     const uint32_t L = blockIdx.x;
     uint32_t head, qb_rev;
     if ((bh & 7u) == 0) {
@@ -773,7 +765,6 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     const uint32_t qspan = (uint32_t)((S - 1) * (uint64_t)a.q_row_stride + D) * 2;
     const uint32_t kspan = (uint32_t)((S - 1) * (uint64_t)a.k_row_stride + D) * 2;
     const uint32_t vspan = (uint32_t)((S - 1) * (uint64_t)a.v_row_stride + D) * 2;
-    const u32x4 qr = rsrc_words(a.q + (size_t)head * a.q_stride, qspan);
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.k + (size_t)head * a.k_stride, kspan);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v + (size_t)head * a.v_stride, vspan);
     float *obase = a.o + (size_t)head * a.o_stride;
@@ -805,7 +796,10 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
     } else {
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) buffer_load_b128_asm(qf[kk], qr, (uint32_t)qrow * qrb + (16 * kk + 8 * hh) * 2);
+        for (int kk = 0; kk < D / 16; ++kk)
+            qf[kk] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   make_rsrc(a.q + (size_t)head * a.q_stride, qspan),
+                                                   (uint32_t)qrow * qrb + (16 * kk + 8 * hh) * 2, 0, 0));
     }
 
     // One query group per workgroup: every wave consumes only its own key slice of each block,
@@ -919,11 +913,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             acc = mfma32<BF>(kf[kk], qf[kk], acc);
         }
         lds_reads_done(kf);
-        // V^T operands, issued once every K read of this step has landed (lds_reads_done orders
-        // them) so their latency hides behind the softmax. ds_read_b64_tr_b16 goes through asm:
-        // the builtin is treated as aliasing the in-flight buffer->LDS loads of later blocks, and
-        // the compiler would drain them (vmcnt(0)) before every read. wait_lds_tied() waits for
-        // these reads and ties the registers to that wait.
+        // V^T operands: their latency hides behind the softmax.
         u32x2 vt[C::MT * 4];
 #pragma unroll
         for (int mt = 0; mt < C::MT; ++mt) {
@@ -1010,7 +1000,6 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         }
         l += ls;
 
-        wait_lds_tied(vt);
 #pragma unroll
         for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
@@ -1070,12 +1059,18 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     };
 
     // Prologue: blocks 0 .. NSTAGE-2 in flight; then Q (issued before them) has landed once at most
-    // their loads are outstanding.
+    // their loads are outstanding. With Q in registers (shared staging, where every wave has at
+    // least one block) the prologue's blocks are issued whatever nblk is (a block past the keys
+    // reads zeros and is never consumed), so the wait count is a constant and the compiler sees Q
+    // complete at it.
     static_for<0, (NSTAGE > 1 ? NSTAGE - 1 : 1)>([&](auto ic) {
         constexpr int I = decltype(ic)::value;
-        if (I < nblk) issue(I, IC<I>{});
+        if (!C::QLDS || I < nblk) issue(I, IC<I>{});
     });
-    with_clamped<0, (NSTAGE > 1 ? NSTAGE - 1 : 1)>(nblk, [&](auto ac) { wait_vm_only<decltype(ac)::value * C::LPW>(); });
+    if constexpr (C::QLDS)
+        with_clamped<0, (NSTAGE > 1 ? NSTAGE - 1 : 1)>(nblk, [&](auto ac) { wait_vm_only<decltype(ac)::value * C::LPW>(); });
+    else
+        wait_vm_only<(NSTAGE > 1 ? NSTAGE - 1 : 1) * C::LPW>();
     if constexpr (C::QLDS) {
         asm volatile("s_barrier" ::: "memory");  // every wave's part of the Q tile has landed
         const uint32_t qt = lds0 + ((XS && xs_role == 1 && s >= xs_w1) ? XS_Q2 : C::Q_OFF);
@@ -1083,7 +1078,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
         for (int kk = 0; kk < D / 16; ++kk)
             qf[kk] = *reinterpret_cast<const NC_LDS(half8) *>((uintptr_t)(qt + SW::slot(32 * qg + c, 2 * kk + hh) * 16));
     }
-    tie_regs(qf);
+    use_now(qf);
     if constexpr (KPF) {
         if (nblk > 0) {
             wait_vm_only<0>();  // block 0's slice
@@ -1344,13 +1339,6 @@ struct RefCfg {
 };
 constexpr int kRefLds = RefCfg<64>::LDS;
 
-template <int N>
-__device__ __forceinline__ void wait_lds_tied_any(u32x2 (&v)[N]) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
-}
-
 // VEC: every Q/K/V slice base is 16-byte aligned (pointers and slice strides; rows of D halves
 // are), so each wave loads a key chunk as one contiguous run of 16-byte segments, stages it in its
 // own LDS region (the next chunk's loads in flight meanwhile) and reads the MFMA operands there:
@@ -1548,9 +1536,6 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
                 vtread(kB + RC::CHUNK, vtb);
                 const half8 pa = softmax(sa, 32 * ch, mrow, l, oacc);
                 const half8 pbb = softmax(sb, 32 * (ch + NW), m1, l1, o1);
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-                for (int i = 0; i < 2 * DT; ++i) asm volatile("" : "+v"(vta[i]), "+v"(vtb[i]));
                 pv(vta, pa, oacc);
                 pv(vtb, pbb, o1);
             }
@@ -1563,7 +1548,6 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
                 u32x2 vta[2 * DT];
                 vtread(kA + RC::CHUNK, vta);
                 const half8 pa = softmax(sa, 32 * ch, mrow, l, oacc);
-                wait_lds_tied_any(vta);
                 pv(vta, pa, oacc);
             }
             // Stream B into A (row-uniform maxima; a stream that saw no chunk has m = -inf, l = O = 0).
@@ -1639,7 +1623,6 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
             const half2v hp = {pb[2 * t], pb[2 * t + 1]};
             l = __builtin_amdgcn_fdot2(hp, ones, l, false);
         }
-        if constexpr (VEC) wait_lds_tied_any(vt);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             half8 va;

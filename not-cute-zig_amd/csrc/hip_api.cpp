@@ -15,6 +15,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "notcute_flash.h"
 
@@ -30,10 +31,14 @@ struct nc_module_st {
     // so a returned nc_function stays valid without the lock.
     std::mutex lock;
     std::unordered_map<std::string, std::unique_ptr<nc_function_st>> functions;
-    // Scratch of the kernels that need one (the pair-split flash kernels), grown on demand and
-    // zeroed when allocated; their exchange counters rely on starting from zero. Guarded by `lock`.
+    // Scratch for callers that launch the pair-split flash kernels by name
+    // (nc_flash_reserve_workspace), zeroed when allocated: their exchange counters rely on starting
+    // from zero. Growing it allocates a larger one and keeps the old one in `retired` until unload,
+    // because graphs captured earlier and by-name callers may still hold its address. Guarded by
+    // `lock`.
     void *workspace = nullptr;
     size_t workspace_bytes = 0;
+    std::vector<void *> retired;
 };
 
 extern "C" const unsigned char nc_embedded_code_object[];
@@ -91,7 +96,7 @@ int fail(int status, const char *what) {
 // Error helpers for the library's other translation units (flash.cpp, noalloc.hip).
 extern "C" int nc_internal_check(int hip_error, const char *what) { return check((hipError_t)hip_error, what); }
 extern "C" int nc_internal_fail(int status, const char *what) { return fail(status, what); }
-// noalloc.hip: the device address of its static scratch on the current device.
+// noalloc.hip: sets up the static scratch on every visible device (device 0 current afterwards).
 extern "C" int nc_internal_noalloc_setup(void);
 
 extern "C" {
@@ -129,7 +134,9 @@ int nc_init(void) {
     if (st) return st;
     st = check(hipSetDevice(0), "hipSetDevice(0)");
     if (st) return st;
-    st = nc_internal_noalloc_setup();  // the static scratch of nc_flash_launch_noalloc on device 0
+    // The static scratch of the pair-split kernels on every visible GPU: its address, and its exchange
+    // counters zeroed (again after an nc_deinit), so that no launch sets anything up later.
+    st = nc_internal_noalloc_setup();
     if (st) return st;
     g_initialized = true;
     return NC_SUCCESS;
@@ -215,26 +222,23 @@ int nc_module_unload(nc_module module) {
     if (!module) return fail(NC_ERROR_INVALID_VALUE, "nc_module_unload: null module");
     int st = NC_SUCCESS;
     if (module->workspace) st = check(hipFree(module->workspace), "hipFree(workspace)");
+    for (void *p : module->retired) {
+        const int s2 = check(hipFree(p), "hipFree(retired workspace)");
+        if (!st) st = s2;
+    }
     int st2 = check(hipModuleUnload(module->mod), "hipModuleUnload");
     delete module;
     return st ? st : st2;
 }
 
-// The module's workspace, at least `bytes` long (used by flash.cpp). A larger one replaces it
-// after the device has finished every launch that may still use the old one; a new workspace is
-// zeroed before it is returned.
+// The module's workspace, at least `bytes` long (used by nc_flash_reserve_workspace). A larger one
+// replaces it as the current workspace; the old one stays allocated until nc_module_unload, since
+// graphs captured earlier and by-name callers may still use its address. A new workspace is zeroed
+// (and the zeroing waited for) before it is returned.
 extern "C" int nc_internal_module_workspace(nc_module module, size_t bytes, void **out) {
     if (!module || !out) return fail(NC_ERROR_INVALID_VALUE, "workspace: null argument");
     std::lock_guard<std::mutex> guard(module->lock);
     if (module->workspace_bytes < bytes) {
-        if (module->workspace) {
-            int st = check(hipDeviceSynchronize(), "hipDeviceSynchronize(workspace)");
-            if (st) return st;
-            st = check(hipFree(module->workspace), "hipFree(workspace)");
-            module->workspace = nullptr;
-            module->workspace_bytes = 0;
-            if (st) return st;
-        }
         void *p = nullptr;
         int st = check(hipMalloc(&p, bytes), "hipMalloc(workspace)");
         if (st) return st;
@@ -245,11 +249,23 @@ extern "C" int nc_internal_module_workspace(nc_module module, size_t bytes, void
             (void)hipFree(p);
             return st;
         }
+        if (module->workspace) module->retired.push_back(module->workspace);
         module->workspace = p;
         module->workspace_bytes = bytes;
     }
     *out = module->workspace;
     return NC_SUCCESS;
+}
+
+// Re-zero the exchange counters of the module's workspaces (current and retired).
+extern "C" int nc_internal_module_reset_workspace(nc_module module) {
+    if (!module) return NC_SUCCESS;
+    std::lock_guard<std::mutex> guard(module->lock);
+    int st = NC_SUCCESS;
+    if (module->workspace) st = check(hipMemset(module->workspace, 0, NC_XS_COUNTER_BYTES), "hipMemset(workspace)");
+    for (void *p : module->retired)
+        if (!st) st = check(hipMemset(p, 0, NC_XS_COUNTER_BYTES), "hipMemset(retired workspace)");
+    return st;
 }
 
 int nc_module_get_function(nc_function *out, nc_module module, const char *name) {

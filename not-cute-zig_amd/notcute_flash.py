@@ -243,6 +243,7 @@ _SIGS = {
         [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, ctypes.c_size_t,
          ctypes.POINTER(FlashOptions), _P]),
     "nc_flash_reserve_workspace": (ctypes.c_int, [_P, ctypes.POINTER(FlashOptions), ctypes.POINTER(_P)]),
+    "nc_flash_reset_scratch": (ctypes.c_int, [_P]),
     "nc_flash_kernel_scratch_bytes": (
         ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(FlashOptions), ctypes.POINTER(_U64)]),
     "nc_benchmark_options_init": (None, [ctypes.POINTER(BenchmarkOptions)]),
@@ -375,6 +376,12 @@ def reserve_workspace(module: "Module", opts: FlashOptions) -> Optional[int]:
     check(lib().nc_flash_reserve_workspace(module.handle, ctypes.byref(opts), ctypes.byref(p)),
           "flash.reserveWorkspace")
     return p.value
+
+
+def reset_scratch(module: Optional["Module"] = None) -> None:
+    """nc_flash_reset_scratch: zero the pair-split exchange counters (static scratch of the current
+    GPU, and `module`'s workspaces) and synchronise; no launch may be in flight."""
+    check(lib().nc_flash_reset_scratch(module.handle if module is not None else None), "flash.resetScratch")
 
 
 # ---------------------------------------------------------------------------------------------

@@ -402,6 +402,25 @@ def test_kernel_scratch_bytes_by_name():
     assert e.value.name == "NotFound"
 
 
+def test_kernel_scratch_bytes_refuses_more_pairs_than_counters():
+    """The counter region holds NC_XS_MAX_PAIRS = 16384 exchange counters: BH=64 S=16384 (64 x 256
+    pairs) is the largest BH=64 shape that fits; one more query block per head (S=16448, 64 x 257
+    pairs) would put counters inside pair 0's partial slot, so the by-name size query refuses it."""
+    from flash_workloads import Workload
+
+    def opts(bh, s):
+        return Workload("x", bh, s, 64, True, 0.125, (("normal", 0, 1),) * 3).options()
+
+    fits = nc.kernel_scratch_bytes("nc_flash_fwd_d64_q1s8p2x_causal", opts(64, 16384))
+    assert fits == 65536 + 16384 * 2 * 8448
+    for name in ("nc_flash_fwd_d64_q1s8p2x_causal", "nc_flash_fwd_d64_q1s8p2x_causal_bf16"):
+        with pytest.raises(nc.NcError) as e:
+            nc.kernel_scratch_bytes(name, opts(64, 16448))
+        assert e.value.name == "InvalidValue"
+    # kernels without scratch have no such limit
+    assert nc.kernel_scratch_bytes("nc_flash_fwd_d64_q1s8p2_causal", opts(64, 16448)) == 0
+
+
 # C struct name of each ctypes mirror. A foreign binding (the Zig `@cImport` of the header that
 # INTEGRATION.md sketches, ctypes here) maps its fields onto exactly these offsets and sizes.
 _ABI_STRUCTS = {

@@ -7,10 +7,10 @@ long causal sequences over few heads (at least 96 query blocks, at most 256 work
 cases here launch the kernel by name with a scratch buffer of their own, on shapes of every kind
 (odd and even block counts, S not a multiple of 32, batch_heads not a multiple of 8, which puts the
 two workgroups of a pair on different XCDs, bf16); the dispatched shapes go through nc_flash_launch
-and the module's workspace. Beyond the oracle, the tests launch repeatedly with the same and with
-changing inputs, alternate shapes that share one scratch buffer (whose counters then overlap), grow
-the module's workspace and replay a HIP graph: a counter left odd or a stale partial would show as
-a wrong row.
+and the library's static scratch. Beyond the oracle, the tests launch repeatedly with the same and
+with changing inputs, alternate shapes that share one scratch buffer (whose counters then overlap),
+capture a module's first launch into a HIP graph, grow the by-name workspace under a captured graph
+and replay graphs: a counter left odd or a stale partial would show as a wrong row.
 """
 
 import numpy as np
@@ -112,7 +112,7 @@ def test_pair_split_parity(gpu, bh, s, dtype):
 
 @pytest.mark.parametrize("bh,s", DISPATCHED, ids=[f"bh{b}_s{s}" for b, s in DISPATCHED])
 def test_pair_split_dispatched(gpu, bh, s):
-    """Shapes the dispatch sends to the pair split, through nc_flash_launch and the module's workspace."""
+    """Shapes the dispatch sends to the pair split, through nc_flash_launch and the static scratch."""
     wl = _wl(bh, s, seed=60 + s + bh)
     sel = nc.select_kernel(wl.options())
     print(f"[case] {wl.describe()} -> {sel.name.decode()} scratch {sel.scratch_bytes}", flush=True)
@@ -203,10 +203,10 @@ def test_pair_split_shapes_share_a_scratch_buffer(gpu):
         scratch.free()
 
 
-def test_pair_split_module_workspace_grows(gpu):
-    """Dispatched shapes in increasing and then decreasing size on one module: the workspace grows
-    (a new zeroed buffer) and is then shared; every output checked on sampled rows."""
-    mod = nc.Module.load_embedded()  # a fresh module: its workspace starts empty
+def test_pair_split_dispatched_sizes_share_the_static_scratch(gpu):
+    """Dispatched shapes in increasing and then decreasing size on a fresh module: all share the
+    GPU's static scratch (their counters overlap); every output checked on sampled rows."""
+    mod = nc.Module.load_embedded()
     try:
         for n, (bh, s) in enumerate([(1, 3072), (2, 4096), (1, 8192), (2, 3100), (1, 8192)]):
             wl = _wl(bh, s, seed=70 + n)
@@ -228,7 +228,6 @@ def test_pair_split_graph_replays(gpu):
     run = Run(wl, q, k, v, o_init)
     stream = nc.Stream()
     try:
-        nc.reserve_workspace(gpu, wl.options())
         run.launch(gpu, stream.handle)
         stream.synchronize()
         eager = run.output()
@@ -249,6 +248,123 @@ def test_pair_split_graph_replays(gpu):
     finally:
         run.free()
         stream.destroy()
+
+
+def test_first_launch_captured_into_a_graph(gpu):
+    """The first nc_flash_launch of a freshly loaded module, of a pair-split shape (BH=1 S=4096
+    causal) and with nothing reserved, captured into a HIP graph: the launch neither allocates nor
+    synchronises, so the capture succeeds; three replays, with eager launches and synchronisation
+    between them, each match the oracle and one another bitwise."""
+    wl = _wl(1, 4096, seed=61)
+    assert nc.select_kernel(wl.options()).name.decode() == XS
+    q, k, v = wl.make_inputs()
+    o_init = np.zeros(wl.length("o"), dtype=np.float32)
+    rows = np.unique(np.concatenate([np.arange(0, wl.seq_len, 29), np.arange(wl.seq_len - 33, wl.seq_len)]))
+    ref = fc.oracle(wl, q, k, v, rows=rows, o_init=o_init)
+    idx = fc.active_index(wl, rows)
+    mod = nc.Module.load_embedded()
+    run = Run(wl, q, k, v, o_init)
+    stream = nc.Stream()
+    try:
+        print(f"[case] {wl.describe()} first launch of a fresh module under capture", flush=True)
+        graph = nc.Graph.capture(stream, lambda: run.launch(mod, stream.handle))
+        try:
+            first = None
+            for i in range(3):
+                run.bufs[3].memset(0)
+                graph.launch(stream)
+                stream.synchronize()
+                out = run.output()
+                fc.assert_parity(out, ref, idx, f"replay {i}")
+                if first is None:
+                    first = out
+                assert np.array_equal(out.view(np.uint32), first.view(np.uint32)), f"replay {i} differs"
+                run.launch(mod, stream.handle)  # eager work between replays
+                stream.synchronize()
+        finally:
+            graph.destroy()
+    finally:
+        run.free()
+        stream.destroy()
+        mod.unload()
+
+
+def test_by_name_workspace_outlives_growth(gpu):
+    """A by-name launch captured into a graph with the workspace reserved for a small shape keeps
+    working after a larger reserve on the same module grows the workspace (the old one is kept until
+    the module is unloaded): replays after the growth, and after eager launches of the larger shape
+    on the new workspace, match the oracle."""
+    small, large = _wl(1, 3072, seed=62), _wl(1, 8192, seed=63)
+    mod = nc.Module.load_embedded()
+    stream = nc.Stream()
+    data = {}
+    try:
+        for wl in (small, large):
+            q, k, v = wl.make_inputs()
+            o_init = np.zeros(wl.length("o"), dtype=np.float32)
+            rows = np.arange(0, wl.seq_len, 47)
+            data[wl.name] = (Run(wl, q, k, v, o_init), fc.oracle(wl, q, k, v, rows=rows, o_init=o_init),
+                             fc.active_index(wl, rows))
+
+        def by_name(wl, ws):
+            run = data[wl.name][0]
+            sel = nc.KernelSelection()
+            sel.block_m = 32
+            args = nc.pack_args(wl.options(), sel, *[b.ptr for b in run.bufs])
+            args.scratch = ws
+            mod.get_function(XS).launch((((wl.seq_len + 31) // 32) * wl.batch_heads,), (512,), [args],
+                                        stream=stream.handle)
+
+        ws_small = nc.reserve_workspace(mod, small.options())
+        assert ws_small
+        graph = nc.Graph.capture(stream, lambda: by_name(small, ws_small))
+        try:
+            ws_large = nc.reserve_workspace(mod, large.options())
+            assert ws_large and ws_large != ws_small
+            assert nc.reserve_workspace(mod, small.options()) == ws_large  # the larger one serves both now
+            for i in range(3):
+                run, ref, idx = data[small.name]
+                run.bufs[3].memset(0)
+                graph.launch(stream)
+                stream.synchronize()
+                fc.assert_parity(run.output(), ref, idx, f"small replay {i}")
+                run, ref, idx = data[large.name]
+                run.bufs[3].memset(0)
+                by_name(large, ws_large)
+                stream.synchronize()
+                fc.assert_parity(run.output(), ref, idx, f"large eager {i}")
+        finally:
+            graph.destroy()
+    finally:
+        for run, _, _ in data.values():
+            run.free()
+        stream.destroy()
+        mod.unload()
+
+
+def test_reset_scratch_restores_the_counters(gpu):
+    """nc_flash_reset_scratch zeroes the exchange counters: launches before and after it agree with
+    the oracle (the counters are even between launches, so a reset between launches changes
+    nothing a later launch sees)."""
+    wl = _wl(2, 4096, seed=64)
+    q, k, v = wl.make_inputs()
+    o_init = np.zeros(wl.length("o"), dtype=np.float32)
+    rows = np.arange(0, wl.seq_len, 31)
+    ref = fc.oracle(wl, q, k, v, rows=rows, o_init=o_init)
+    idx = fc.active_index(wl, rows)
+    run = Run(wl, q, k, v, o_init)
+    try:
+        for i in range(2):
+            run.launch(gpu)
+            fc.assert_parity(run.output(), ref, idx, f"before reset, launch {i}")
+        nc.reset_scratch(gpu)
+        nc.reset_scratch()
+        for i in range(2):
+            run.bufs[3].memset(0)
+            run.launch(gpu)
+            fc.assert_parity(run.output(), ref, idx, f"after reset, launch {i}")
+    finally:
+        run.free()
 
 
 def test_pair_split_matches_unsplit_kernel(gpu):
