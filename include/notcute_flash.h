@@ -156,6 +156,11 @@ int nc_stream_synchronize(nc_stream stream);
 
 /* Event (src/cuda.zig:427-460). */
 int nc_event_create(nc_event *out);
+/* Extension: an event used only to time the stream between two records (nc_event_elapsed). Its
+ * record skips the system-scope cache writeback and invalidate that a default event's record
+ * performs (hipEventDisableSystemFence), so the event pair brackets the kernels between them and not
+ * a cache flush; work after it still runs in stream order. */
+int nc_event_create_timing(nc_event *out);
 int nc_event_destroy(nc_event ev);
 int nc_event_record(nc_event ev, nc_stream stream);
 int nc_event_synchronize(nc_event ev);

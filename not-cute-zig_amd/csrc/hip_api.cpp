@@ -374,6 +374,14 @@ int nc_event_create(nc_event *out) {
     return st;
 }
 
+int nc_event_create_timing(nc_event *out) {
+    if (!out) return fail(NC_ERROR_INVALID_VALUE, "nc_event_create_timing: null output");
+    hipEvent_t e = nullptr;
+    int st = check(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreateWithFlags");
+    *out = e;
+    return st;
+}
+
 int nc_event_destroy(nc_event ev) { return check(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy"); }
 
 int nc_event_record(nc_event ev, nc_stream stream) {

@@ -213,6 +213,7 @@ _SIGS = {
     "nc_stream_destroy": (ctypes.c_int, [_P]),
     "nc_stream_synchronize": (ctypes.c_int, [_P]),
     "nc_event_create": (ctypes.c_int, [ctypes.POINTER(_P)]),
+    "nc_event_create_timing": (ctypes.c_int, [ctypes.POINTER(_P)]),
     "nc_event_destroy": (ctypes.c_int, [_P]),
     "nc_event_record": (ctypes.c_int, [_P, _P]),
     "nc_event_synchronize": (ctypes.c_int, [_P]),
@@ -535,9 +536,13 @@ class Stream:
 
 
 class Event:
-    def __init__(self):
+    def __init__(self, timing_only: bool = False):
+        """timing_only: nc_event_create_timing (no system-scope cache flush when recorded)."""
         h = ctypes.c_void_p()
-        check(lib().nc_event_create(ctypes.byref(h)), "Event.create")
+        if timing_only:
+            check(lib().nc_event_create_timing(ctypes.byref(h)), "Event.createTiming")
+        else:
+            check(lib().nc_event_create(ctypes.byref(h)), "Event.create")
         self.handle = int(h.value)
 
     def record(self, stream: Optional[int] = None) -> None:
