@@ -330,8 +330,9 @@ int nc_flash_launch_noalloc(nc_module module, const uint16_t *q, size_t q_len, c
 
 /* Extension (no counterpart in the reference, whose kernels use no scratch memory), for callers that
  * launch the selected kernel by name themselves: make the module's workspace large enough for a
- * launch with these options (allocating and zeroing device memory when it must grow) and store it in
- * *workspace (may be NULL); they put it in nc_flash_kernel_args.scratch. Stores NULL, allocating
+ * launch with these options (allocating and zeroing device memory, and synchronising the device,
+ * when it must grow) and store it in *workspace (may be NULL); they put it in
+ * nc_flash_kernel_args.scratch. Stores NULL, allocating
  * nothing, when the selected kernel needs no scratch. A returned workspace stays valid until
  * nc_module_unload: growing it allocates a new one and keeps the old. nc_flash_launch does not use it. */
 int nc_flash_reserve_workspace(nc_module module, const nc_flash_options *opts, void **workspace);

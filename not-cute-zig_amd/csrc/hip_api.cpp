@@ -239,6 +239,12 @@ extern "C" int nc_internal_module_workspace(nc_module module, size_t bytes, void
     if (!module || !out) return fail(NC_ERROR_INVALID_VALUE, "workspace: null argument");
     std::lock_guard<std::mutex> guard(module->lock);
     if (module->workspace_bytes < bytes) {
+        // room to keep the current workspace before anything is allocated (no throw past the C ABI)
+        try {
+            module->retired.reserve(module->retired.size() + 1);
+        } catch (...) {
+            return fail(NC_ERROR_OUT_OF_MEMORY, "workspace: host allocation failed");
+        }
         void *p = nullptr;
         int st = check(hipMalloc(&p, bytes), "hipMalloc(workspace)");
         if (st) return st;
@@ -249,7 +255,7 @@ extern "C" int nc_internal_module_workspace(nc_module module, size_t bytes, void
             (void)hipFree(p);
             return st;
         }
-        if (module->workspace) module->retired.push_back(module->workspace);
+        if (module->workspace) module->retired.push_back(module->workspace);  // capacity reserved above
         module->workspace = p;
         module->workspace_bytes = bytes;
     }
