@@ -289,6 +289,52 @@ def test_first_launch_captured_into_a_graph(gpu):
         mod.unload()
 
 
+_FIRST_LAUNCH_PROGRAM = r"""
+import sys
+import numpy as np
+import flashcheck as fc
+import notcute_flash as nc
+from flash_workloads import Workload
+nc.load_library()
+nc.init()
+mod = nc.Module.load_embedded()
+wl = Workload("xs_first", 1, 4096, 64, True, 0.125, (("normal", 0.0, 1.0),) * 3, seed=65)
+assert nc.select_kernel(wl.options()).name.decode() == "nc_flash_fwd_d64_q1s8p2x_causal"
+q, k, v = wl.make_inputs()
+o_init = np.zeros(wl.length("o"), dtype=np.float32)
+rows = np.arange(0, wl.seq_len, 37)
+ref = fc.oracle(wl, q, k, v, rows=rows, o_init=o_init)
+bufs = [nc.DeviceBuffer.from_array(x) for x in (q, k, v, o_init)]
+stream = nc.Stream()
+graph = nc.Graph.capture(stream, lambda: nc.flash_launch(mod, *bufs, wl.options(), stream=stream.handle))
+for i in range(3):
+    bufs[3].memset(0)
+    graph.launch(stream)
+    stream.synchronize()
+    fc.assert_parity(bufs[3].download(np.float32, wl.length("o")), ref, fc.active_index(wl, rows), f"replay {i}")
+graph.destroy()
+print("first-launch capture ok", flush=True)
+"""
+
+
+def test_first_launch_of_a_process_captured(gpu):
+    """In a fresh process, the very first flash launch (a pair-split shape, BH=1 S=4096 causal, no
+    reserve, no eager launch before it) is captured into a HIP graph and replayed three times,
+    each replay checked against the oracle."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join(os.path.join(root, d) for d in ("not-cute-zig_amd", "oracle", "tests"))
+    print("[case] first launch of a fresh process, captured (subprocess)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_LAUNCH_PROGRAM], env=env, capture_output=True, text=True,
+                       timeout=110)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "first-launch capture ok" in r.stdout
+
+
 def test_by_name_workspace_outlives_growth(gpu):
     """A by-name launch captured into a graph with the workspace reserved for a small shape keeps
     working after a larger reserve on the same module grows the workspace (the old one is kept until
