@@ -529,6 +529,13 @@ struct IC {
     static constexpr int value = N;
 };
 
+// x from another lane of the same 16-lane row, selected by the DPP control CTRL (quad_perm,
+// row_half_mirror, row_newbcast); every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
 // Calls f(IC<I>{}) for I = B .. E-1 (compile-time loop index).
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
@@ -1219,6 +1226,41 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
             return;
         }
         wait_vm_barrier<0>();
+        if constexpr (DC == 16 && NS == 8 && C::BM * DC == C::NT) {
+            // One thread per (query, 4 columns): a query's 16 threads are one 16-lane DPP row. Lanes
+            // j and j+8 of the row read split j's (m, l); the row's max M and L = sum_j w_j l_j
+            // (w_j = exp2(m_j - M)) come from three DPP steps each, and lane j's normalised weight
+            // w_j / L is broadcast to the row once per split (row_newbcast), so each thread forms
+            // one exponential instead of eight. The reductions use commutative pairings only, so
+            // every lane of a row holds bitwise the same M and L.
+            const int qi = tid >> 4, ch = tid & 15;
+            floatx4 pj[NS];  // read first, so the LDS reads overlap the weights' DPP chain
+#pragma unroll
+            for (int j = 0; j < NS; ++j) pj[j] = *part(j, qi, ch);
+            const float2v mlj = mlb[qi * NS + (ch & 7)];
+            float mx = mlj[0];
+            mx = fmaxf(mx, dpp_f32<0xB1>(mx));   // quad_perm [1,0,3,2]
+            mx = fmaxf(mx, dpp_f32<0x4E>(mx));   // quad_perm [2,3,0,1]
+            mx = fmaxf(mx, dpp_f32<0x141>(mx));  // row_half_mirror: the two quads of each half-row
+            const float wj = __builtin_amdgcn_exp2f(mlj[0] - mx);  // 0 for a split that saw no key
+            float den = wj * mlj[1];
+            den += dpp_f32<0xB1>(den);
+            den += dpp_f32<0x4E>(den);
+            den += dpp_f32<0x141>(den);
+            const float wn = wj * __builtin_amdgcn_rcpf(den);
+            // the partial reads complete here, not later inside the store's row test
+            asm volatile("" ::"v"(wn), "v"(pj[0]), "v"(pj[1]), "v"(pj[2]), "v"(pj[3]), "v"(pj[4]), "v"(pj[5]),
+                         "v"(pj[6]), "v"(pj[7]));
+            floatx4 res = dpp_f32<0x150>(wn) * pj[0];  // row_newbcast:0
+            static_for<1, NS>([&](auto jc) {
+                constexpr int J = decltype(jc)::value;
+                res += dpp_f32<0x150 + J>(wn) * pj[J];  // row_newbcast:J
+            });
+            const int row = q0 + qi;
+            if (row < S) store_o(reinterpret_cast<floatx4 *>(obase + (size_t)row * ors + 4 * ch), res);
+            NC_TL_END()
+            return;
+        }
         for (int u = tid; u < C::BM * DC; u += C::NT) {
             const int qi = u / DC, ch = u % DC;
             const int row = q0 + qi;
