@@ -278,6 +278,11 @@ typedef struct nc_flash_kernel_args {
     uint32_t batch_heads;
     uint32_t num_q_blocks; /* ceil(seq_len / block_m) */
     void *scratch;         /* device scratch of kernels that need one (selection.scratch_bytes), else NULL */
+    /* Performance only, results do not depend on it: the number of the grid's last workgroups that
+     * order their waves by remaining work so that co-resident ones finish together (non-causal
+     * shared-staging kernels; 0: none). nc_flash_pack_args sets it from the current device's CU count
+     * when the grid has more workgroups than the device has CUs. */
+    uint32_t balance_tail;
 } nc_flash_kernel_args;
 
 /* Layout of the scratch of the pair-split kernels (selection.scratch_bytes): a fixed region of

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdint>
 #include <cstring>
@@ -198,19 +199,61 @@ const char *reference_kernel(const nc_flash_options &o) {
 // best, where the threshold rules they replace averaged 1.052x and 1.023x; on 50 bf16 shapes each,
 // 1.010x and 1.006x (thresholds: 1.046x and 1.049x). The bf16 twins have the same instruction
 // stream and use the same model.
+// `balance`: the non-causal kernel orders its waves by remaining work in the grid's last
+// wg_per_cu * CUs workgroups (nc_flash_kernel_args.balance_tail), where that was measured faster.
 struct PipeModel {
     uint32_t d, nq, ns, wg_per_cu, waves_per_simd;
     float a, rho, lat, tau;
+    bool balance;
 };
 const PipeModel kPipeModels[] = {
-    {64, 8, 1, 2, 2, 2.3643f, 3.7198f, 0.5110f, 0.2491f},  // q8s1p2t2
-    {64, 4, 1, 4, 1, 1.9664f, 4.3401f, 0.4105f, 0.2735f},  // q4s1p2t2
-    {64, 2, 4, 2, 2, 2.0057f, 2.5877f, 0.5000f, 0.3134f},  // q2s4p2
-    {64, 1, 8, 1, 2, 0.4023f, 2.9534f, 0.3000f, 0.3978f},  // q1s8p2
-    {32, 4, 1, 5, 1, 2.0217f, 2.5512f, 0.3837f, 0.1863f},  // q4s1p3
-    {32, 2, 4, 2, 2, 1.7707f, 2.6393f, 0.5084f, 0.2020f},  // q2s4p2
-    {32, 1, 8, 2, 2, 1.6322f, 1.5959f, 0.5621f, 0.2483f},  // q1s8p2
+    {64, 8, 1, 2, 2, 2.3643f, 3.7198f, 0.5110f, 0.2491f, true},    // q8s1p2t2
+    {64, 4, 1, 4, 1, 1.9664f, 4.3401f, 0.4105f, 0.2735f, true},    // q4s1p2t2
+    {64, 2, 4, 2, 2, 2.0057f, 2.5877f, 0.5000f, 0.3134f, true},    // q2s4p2
+    {64, 1, 8, 1, 2, 0.4023f, 2.9534f, 0.3000f, 0.3978f, false},   // q1s8p2
+    {32, 4, 1, 5, 1, 2.0217f, 2.5512f, 0.3837f, 0.1863f, false},   // q4s1p3
+    {32, 2, 4, 2, 2, 1.7707f, 2.6393f, 0.5084f, 0.2020f, true},    // q2s4p2
+    {32, 1, 8, 2, 2, 1.6322f, 1.5959f, 0.5621f, 0.2483f, false},   // q1s8p2
 };
+
+// CUs of the current device, read once per device (0 without one).
+uint32_t device_cu_count() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<uint32_t> cus[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    uint32_t n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) return 0;
+        n = (uint32_t)c;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// nc_flash_kernel_args.balance_tail for a selection: the last wg_per_cu * CUs workgroups of a
+// non-causal grid on a kernel marked `balance`, once the grid holds more workgroups than the device
+// has CUs (with one workgroup per CU there is nothing to balance, and the priority changes were
+// measured to cost up to 4 % there); else 0.
+uint32_t balance_tail_for(const nc_flash_options &o, const nc_flash_kernel_selection &sel) {
+    if (o.causal || !sel.name) return 0;
+    const Variant *v = nullptr;
+    for (const auto &x : kVariants)
+        if (x.name == sel.name) {  // a selection's name points into the table
+            v = &x;
+            break;
+        }
+    if (!v || v->family != Family::kPipe || v->nq == 1) return 0;
+    const PipeModel *m = nullptr;
+    for (const auto &pm : kPipeModels)
+        if (pm.d == v->d && pm.nq == v->nq && pm.ns == v->ns) m = &pm;
+    if (!m || !m->balance) return 0;
+    const uint64_t grid = (uint64_t)sel.grid[0] * sel.grid[1] * sel.grid[2];
+    const uint32_t cus = device_cu_count();
+    if (cus == 0 || grid <= cus) return 0;
+    return (uint32_t)std::min<uint64_t>(grid, (uint64_t)cus * m->wg_per_cu);
+}
 
 // Sequential 32-key tiles of the busiest wave of query block qb.
 uint64_t pipe_steps(const Variant &v, uint64_t S, bool causal, uint64_t qb) {
@@ -445,6 +488,7 @@ int nc_flash_pack_args(const nc_flash_options *opts, const nc_flash_kernel_selec
     out->o_row_stride = row_stride_of(op.o_row_stride, op.head_dim);
     out->batch_heads = (uint32_t)op.batch_heads;
     out->num_q_blocks = (uint32_t)((op.seq_len + sel->block_m - 1) / sel->block_m);
+    out->balance_tail = balance_tail_for(op, *sel);
     return NC_SUCCESS;
 }
 

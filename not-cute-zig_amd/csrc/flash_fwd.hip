@@ -813,6 +813,12 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // so each wave stages that slice itself and the key loop needs no barrier; a wave
     // runs only over the blocks where its slice has visible keys.
     constexpr bool PRIV = (NQ == 1);
+    // Non-causal shared staging: co-resident workgroups of equal work, balanced by wave priority at
+    // the end of the grid (the step below). Workgroups before the balancing tail run above it
+    // (priority 3), which keeps the arbiter's oldest-first order between them and the tail.
+    constexpr bool BALANCE = !PRIV && !CAUSAL;
+    const bool balancing = BALANCE && a.balance_tail != 0u && L + a.balance_tail >= gridDim.x;
+    if (BALANCE && a.balance_tail != 0u && !balancing) __builtin_amdgcn_s_setprio(3);
     const int kv_end = CAUSAL ? min(S, q0 + C::BM) : S;
     int nblk = (kv_end + C::BN - 1) / C::BN;
     if constexpr (XS) {
@@ -1027,6 +1033,22 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // sub-tiles.
     auto step = [&](int blk, auto stage_c) {
         constexpr int ST = decltype(stage_c)::value;
+        if constexpr (BALANCE) {
+            // The grid's last workgroups (balance_tail of them) share their CUs with each other to
+            // the end. The issue arbiter favours older waves, so of two co-resident workgroups with
+            // equal work the older finished first and the younger ran its last third alone at half
+            // the CU's waves; ordering waves by remaining key blocks (priority 2 above half, 1 above
+            // 3/16, else 0) keeps such workgroups level, so they finish together.
+            if (balancing) {
+                const int rem32 = (nblk - blk) * 32;
+                if (rem32 >= 16 * nblk)
+                    __builtin_amdgcn_s_setprio(2);
+                else if (rem32 >= 6 * nblk)
+                    __builtin_amdgcn_s_setprio(1);
+                else
+                    __builtin_amdgcn_s_setprio(0);
+            }
+        }
         if constexpr (PRIV && NSTAGE == 1) {
             // Private single stage: the wave's reads of the previous block are complete (their
             // results were consumed), so it refills the stage with this block and waits for it.

@@ -106,6 +106,7 @@ class KernelArgs(ctypes.Structure):
         ("batch_heads", ctypes.c_uint32),
         ("num_q_blocks", ctypes.c_uint32),
         ("scratch", ctypes.c_void_p),
+        ("balance_tail", ctypes.c_uint32),
     ]
 
 

@@ -211,6 +211,22 @@ def test_pack_args_resolves_row_strides():
     assert nc.KernelArgs.scale.offset == 80 and nc.KernelArgs.causal.offset == 84
 
 
+def test_pack_args_balance_tail_needs_a_device():
+    """The balancing tail comes from the current device's CU count; a causal grid, the private-staging
+    kernels and a process without a GPU get 0 (the field only orders waves, never changes results)."""
+    from flash_workloads import CONFIGS
+
+    for key in ("c3", "c5"):
+        opts = CONFIGS[key].options()
+        a = nc.pack_args(opts, nc.select_kernel(opts), 0x1000, 0x2000, 0x3000, 0x4000)
+        assert a.balance_tail == 0, key
+    if nc.device_count() == 0:
+        opts = CONFIGS["c4"].options()
+        a = nc.pack_args(opts, nc.select_kernel(opts), 0x1000, 0x2000, 0x3000, 0x4000)
+        assert a.balance_tail == 0
+    assert nc.KernelArgs.balance_tail.offset == 136 and ctypes.sizeof(nc.KernelArgs) == 144
+
+
 def test_launch_validates_before_touching_the_module():
     lib = nc.load_library()
     bad = nc.options(batch_heads=1, seq_len=16, head_dim=24)
