@@ -628,6 +628,32 @@ struct PipeCfg {
     static constexpr int MT = D < 32 ? 1 : D / 32;
 };
 
+// What one workgroup of the pipelined body computes: query block nqb-1-qb_rev of slice `head`
+// (qb_rev counts from the last, heaviest causal block), and L, its index in the launch, which
+// decides whether it is in the end-of-grid balancing tail (nc_flash_kernel_args.balance_tail).
+struct PipeSlot {
+    uint32_t L, head, qb_rev;
+};
+
+// The dispatched kernels' mapping of launch index L to its slot. Workgroups are dealt round-robin
+// to the 8 XCDs (L mod 8), so with batch_heads a multiple of 8 each XCD takes whole slices
+// (batch_heads/8 of them): every K/V slice is read through one XCD's L2. Within an XCD the query
+// blocks go heaviest (causal) first.
+__device__ __forceinline__ PipeSlot pipe_slot(uint32_t L, uint32_t bh) {
+    if ((bh & 7u) == 0) {
+        const uint32_t hpx = bh >> 3, x = L & 7u, idx = L >> 3;
+        return PipeSlot{L, x * hpx + idx % hpx, idx / hpx};
+    }
+    return PipeSlot{L, L % bh, L / bh};
+}
+
+// LDS the pipelined body needs (the pair-split kernels add a second Q tile and the exchange words).
+template <int D, int NQ, int NS, int NSTAGE, int SUB, bool XS>
+constexpr int pipe_lds_bytes() {
+    using C = PipeCfg<D, NQ, NS, NSTAGE, SUB>;
+    return XS ? C::LDS_BYTES + C::BM * D * 2 + 16 : C::LDS_BYTES;
+}
+
 // Per-wave timeline stamps, compiled only into the timeline code object (-DNC_TIMELINE; the product
 // kernels carry none) and only into the pipelined kernels that use no scratch memory (the pair-split
 // kernels exchange their partials through it). With a.scratch set (bit 0 cleared), each wave writes
@@ -655,7 +681,7 @@ struct PipeCfg {
         const uint64_t tl_end2 = __builtin_amdgcn_s_memtime(), tl_r1 = __builtin_amdgcn_s_memrealtime(); \
         if (lane == 0 && a.scratch != nullptr) {                                                         \
             uint64_t *st = reinterpret_cast<uint64_t *>((uintptr_t)a.scratch & ~(uintptr_t)1) +         \
-                           ((size_t)blockIdx.x * C::NW + (uint32_t)w) * NC_TIMELINE_WORDS;               \
+                           ((size_t)L * C::NW + (uint32_t)w) * NC_TIMELINE_WORDS;                        \
             st[0] = tl_entry; st[1] = tl_loop0; st[2] = tl_loop1; st[3] = tl_end; st[4] = tl_end2;       \
             st[5] = tl_r0; st[6] = tl_r1;                                                                \
             st[7] = __builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11)) |                             \
@@ -670,16 +696,17 @@ struct PipeCfg {
 #define NC_TL_END()
 #endif
 
-template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB, bool BF, bool XS = false>
-__device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &a) {
+// slot_of(batch_heads) gives the workgroup's PipeSlot (called once the arguments are checked).
+template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB, bool BF, bool XS = false, typename SlotFn>
+__device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &a, char *smem, SlotFn &&slot_of) {
     using C = PipeCfg<D, NQ, NS, NSTAGE, SUB>;
     using SW = Swz<D>;
     static_assert(NSTAGE >= 1 && NSTAGE <= 8, "ring depth");
     static_assert(!XS || (NQ == 1 && NS == 8 && SUB == 1 && CAUSAL), "pair split: causal private staging");
-    // XS: a second Q tile (the B workgroup's second query block) and two words for the pair exchange.
+    // XS: a second Q tile (the B workgroup's second query block) and two words for the pair exchange
+    // (pipe_lds_bytes sizes the caller's LDS buffer to match).
     constexpr int XS_Q2 = C::LDS_BYTES;
     constexpr int XS_WORDS = XS_Q2 + C::BM * D * 2;
-    __shared__ __attribute__((aligned(16))) char smem[XS ? XS_WORDS + 16 : C::LDS_BYTES];
 
     if (a.head_dim != (uint64_t)D || a.seq_len == 0) return;
     if (XS && a.scratch == nullptr) return;  // the host always passes the pair-exchange buffer
@@ -691,16 +718,8 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // host API refuses such shapes (nc_flash_kernel_scratch_bytes), and a by-name launch of one
     // writes nothing.
     if (XS && (uint64_t)bh * (nqb >> 1) > NC_XS_MAX_PAIRS) return;
-    const uint32_t L = blockIdx.x;
-    uint32_t head, qb_rev;
-    if ((bh & 7u) == 0) {
-        const uint32_t hpx = bh >> 3, x = L & 7u, idx = L >> 3;
-        head = x * hpx + idx % hpx;
-        qb_rev = idx / hpx;
-    } else {
-        head = L % bh;
-        qb_rev = L / bh;
-    }
+    const PipeSlot slot = slot_of(bh);
+    const uint32_t L = slot.L, head = slot.head, qb_rev = slot.qb_rev;
     const int qb = (int)(nqb - 1u - qb_rev);
 
     const int tid = threadIdx.x;
@@ -1368,6 +1387,13 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     NC_TL_END()
 }
 
+// A dispatched pipelined kernel: its LDS, and launch index blockIdx.x mapped by pipe_slot.
+template <int D, int NQ, int NS, bool CAUSAL, int NSTAGE, int SUB, bool BF, bool XS = false>
+__device__ __forceinline__ void flash_fwd_pipe_kernel(const nc_flash_kernel_args &a) {
+    __shared__ __attribute__((aligned(16))) char smem[pipe_lds_bytes<D, NQ, NS, NSTAGE, SUB, XS>()];
+    flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, BF, XS>(a, smem, [](uint32_t bh) { return pipe_slot(blockIdx.x, bh); });
+}
+
 // ---------------------------------------------------------------------------------------------
 // Reference-ABI entry points: the kernel symbols the reference's code object exports
 // (flash_attention_fwd_{v2,opt,h64,h64_bn32,h64_causal} and the legacy flash_attention_fwd,
@@ -1402,6 +1428,14 @@ struct RefCfg {
     static constexpr int SEG = 32 * (D / 8) / 64;    // 16-byte segments of a chunk per lane
 };
 constexpr int kRefLds = RefCfg<64>::LDS;
+// Grid size (workgroups) from which the 128-thread d=64 launches take four 16-row blocks per
+// working workgroup (flash_fwd_refabi). Measured on MI355X with the reference's grid: from 1536
+// workgroups (384 working ones) it was 1.13-2.1x faster on every shape tried; at 1024 it was
+// mixed (S=2048 faster, S=1024 10-15 % slower) and at 512-768 slower (c3 19.6 against 14.5 us).
+#ifndef NC_REF_COARSE_MIN_WORKGROUPS
+#define NC_REF_COARSE_MIN_WORKGROUPS 1536
+#endif
+constexpr uint64_t kRefCoarseMinWorkgroups = NC_REF_COARSE_MIN_WORKGROUPS;
 
 // VEC: every Q/K/V slice base is 16-byte aligned (pointers and slice strides; rows of D halves
 // are), so each wave loads a key chunk as one contiguous run of 16-byte segments, stages it in its
@@ -1757,6 +1791,45 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
         flash_fwd_refabi_body<decltype(dc)::value, decltype(vc)::value != 0>(q, k, v, o, S, q_stride, k_stride, v_stride,
                                                                               o_stride, scale, cz, smem);
     };
+    // Large d=64 grids of two-wave workgroups (the reference's 128-thread launches): one workgroup
+    // of each group of four consecutive 16-row blocks computes the group's 64 rows with the
+    // pipelined body (two 32-row query waves sharing each staged K/V block), and the other three
+    // return. Each K/V byte staged then serves 64 queries instead of 16. Which workgroup of a group
+    // works rotates with the group and the slice, so the working ones spread over the XCDs. Only
+    // for a grid of exactly ceil(S/16) blocks per slice (so no row outside the launch is written)
+    // and 16-byte aligned Q/K/V/O slices (the pipelined body's float4 O stores).
+    const bool o_vec = (reinterpret_cast<uintptr_t>(o) & 15u) == 0 && (o_stride & 3u) == 0;
+    if (head_dim == 64 && vec && o_vec && blockDim.x == 128 && gridDim.x == (seq_len + 15) / 16 &&
+        (uint64_t)gridDim.x * gridDim.y >= kRefCoarseMinWorkgroups) {
+        static_assert(pipe_lds_bytes<64, 2, 1, 2, 2, false>() <= kRefLds, "the pipelined body fits the LDS");
+        const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 2;
+        const uint32_t sz = gx - 4u * m < 4u ? gx - 4u * m : 4u;
+        if (bx != 4u * m + (by + m) % sz) return;
+        nc_flash_kernel_args a = {};
+        a.q = q;
+        a.k = k;
+        a.v = v;
+        a.o = o;
+        a.seq_len = seq_len;
+        a.head_dim = 64;
+        a.q_stride = q_stride;
+        a.k_stride = k_stride;
+        a.v_stride = v_stride;
+        a.o_stride = o_stride;
+        a.scale = scale;
+        a.causal = cz ? 1u : 0u;
+        a.q_row_stride = a.k_row_stride = a.v_row_stride = a.o_row_stride = 64;
+        a.batch_heads = gridDim.y;
+        a.num_q_blocks = (uint32_t)((seq_len + 63) / 64);
+        // group m computes 64-row block m; causal blocks come heaviest first, as in the
+        // 16-row body, since qb_rev counts from the last block
+        auto slot = [&](uint32_t) { return PipeSlot{0u, by, m}; };
+        if (cz)
+            flash_fwd_pipe_body<64, 2, 1, true, 2, 2, false>(a, smem, slot);
+        else
+            flash_fwd_pipe_body<64, 2, 1, false, 2, 2, false>(a, smem, slot);
+        return;
+    }
     if (head_dim == 64) {
         if (vec) run(IC<64>{}, IC<1>{}); else run(IC<64>{}, IC<0>{});
     } else if (D64_ONLY) {
@@ -1859,21 +1932,21 @@ extern "C" __global__ __launch_bounds__(768) void nc_util_mfma_ceiling(const hal
 // Each instantiation defines NAME (f16) and NAME_bf16.
 #define NC_FLASH_PIPE_KERNEL(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB)                              \
     extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME(nc_flash_kernel_args a) {        \
-        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, false>(a);                         \
+        flash_fwd_pipe_kernel<D, NQ, NS, CAUSAL, NSTAGE, SUB, false>(a);                         \
     }                                                                                          \
     extern "C" __global__ __launch_bounds__(NQ * NS * 64) void NAME##_bf16(nc_flash_kernel_args a) { \
-        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, true>(a);                          \
+        flash_fwd_pipe_kernel<D, NQ, NS, CAUSAL, NSTAGE, SUB, true>(a);                          \
     }
 // With a register budget held to WPE waves per SIMD (512 / WPE VGPRs per wave): two 8-wave
 // workgroups of the 70 KB-LDS variants share a CU only if each wave fits in 128 VGPRs.
 #define NC_FLASH_PIPE_KERNEL_WPE(NAME, D, NQ, NS, CAUSAL, NSTAGE, SUB, WPE)                             \
     extern "C" __global__ __launch_bounds__(NQ * NS * 64) __attribute__((amdgpu_waves_per_eu(WPE)))     \
     void NAME(nc_flash_kernel_args a) {                                                                 \
-        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, false>(a);                                  \
+        flash_fwd_pipe_kernel<D, NQ, NS, CAUSAL, NSTAGE, SUB, false>(a);                                  \
     }                                                                                                   \
     extern "C" __global__ __launch_bounds__(NQ * NS * 64) __attribute__((amdgpu_waves_per_eu(WPE)))     \
     void NAME##_bf16(nc_flash_kernel_args a) {                                                          \
-        flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, true>(a);                                   \
+        flash_fwd_pipe_kernel<D, NQ, NS, CAUSAL, NSTAGE, SUB, true>(a);                                   \
     }
 
 // Pipelined variants: q = query waves (32 rows each), s = key-split waves, p = LDS ring depth.
@@ -1888,10 +1961,10 @@ NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d64_q1s8p2_causal, 64, 1, 8, true, 2, 1)
 // Pair split (x): causal query blocks p and nqb-1-p shared by two workgroups that exchange partials.
 #define NC_FLASH_XS_KERNEL(NAME, D)                                                                     \
     extern "C" __global__ __launch_bounds__(512) void NAME(nc_flash_kernel_args a) {                     \
-        flash_fwd_pipe_body<D, 1, 8, true, 2, 1, false, true>(a);                                       \
+        flash_fwd_pipe_kernel<D, 1, 8, true, 2, 1, false, true>(a);                                       \
     }                                                                                                   \
     extern "C" __global__ __launch_bounds__(512) void NAME##_bf16(nc_flash_kernel_args a) {              \
-        flash_fwd_pipe_body<D, 1, 8, true, 2, 1, true, true>(a);                                        \
+        flash_fwd_pipe_kernel<D, 1, 8, true, 2, 1, true, true>(a);                                        \
     }
 NC_FLASH_XS_KERNEL(nc_flash_fwd_d64_q1s8p2x_causal, 64)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q4s1p3_full, 32, 4, 1, false, 3, 1)

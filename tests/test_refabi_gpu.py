@@ -114,3 +114,73 @@ def test_reference_symbol_other_block_sizes(gpu):
     for name in sorted(REF_KERNELS):
         out = launch_reference_way(gpu, name, 64, bad, q, k, v, o_init)
         assert np.array_equal(out.view(np.uint32), o_init.view(np.uint32)), name
+
+
+# Grids of at least 1536 workgroups on the 128-thread d=64 symbols: one workgroup of each group of
+# four 16-row blocks computes the group's 64 rows with the pipelined body (flash_fwd_refabi). S = 8200
+# and 1040 leave a last group of one block; the rotation of the working workgroup covers every group.
+COARSE_CASES = [
+    Workload("rc_6x4096_c", 6, 4096, 64, True, 0.125, (("normal", 0.0, 1.0),) * 3, seed=41),
+    Workload("rc_6x4096_n", 6, 4096, 64, False, 0.125, (("normal", 0.0, 1.0),) * 3, seed=42),
+    Workload("rc_3x8200_c", 3, 8200, 64, True, 0.125, (("normal", 0.0, 2.0),) * 3, seed=43),
+    Workload("rc_24x1040_n", 24, 1040, 64, False, -0.2, (("normal", 0.0, 1.0),) * 3, seed=44),
+]
+
+
+def _sampled(wl, seed):
+    from flash_workloads import sample_rows
+
+    return sample_rows(wl.seq_len, extra=24, seed=seed)
+
+
+@pytest.mark.parametrize("name", ["flash_attention_fwd_h64_bn32", "flash_attention_fwd_v2"])
+@pytest.mark.parametrize("wl", COARSE_CASES, ids=lambda w: w.name)
+def test_reference_symbol_large_grid(gpu, name, wl):
+    grid = (wl.seq_len + 15) // 16 * wl.batch_heads
+    print(f"[case] {name} threads=128 {wl.describe()} grid={grid}", flush=True)
+    assert grid >= 1536
+    q, k, v = wl.make_inputs()
+    o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
+    rows = _sampled(wl, 5)
+    ref = fc.oracle(wl, q, k, v, rows=rows, o_init=o_init)
+    out = launch_reference_way(gpu, name, 128, wl, q, k, v, o_init)
+    fc.assert_parity(out, ref, fc.active_index(wl, rows), f"{name}/{wl.name}")
+    fc.assert_pads_untouched(out, o_init, wl, f"{name}/{wl.name}")
+
+
+def test_reference_symbol_large_grid_fallbacks(gpu):
+    """A large grid whose O slices are not float4 aligned takes the 16-row body (same results); one
+    narrower than ceil(S/16) blocks writes only the rows its blocks cover, like the reference."""
+    wl = Workload("rc_odd_o", 6, 4096, 64, False, 0.125, (("normal", 0.0, 1.0),) * 3, seed=45,
+                  o_stride=4096 * 64 + 2)
+    q, k, v = wl.make_inputs()
+    o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
+    rows = _sampled(wl, 6)
+    ref = fc.oracle(wl, q, k, v, rows=rows, o_init=o_init)
+    out = launch_reference_way(gpu, "flash_attention_fwd_h64_bn32", 128, wl, q, k, v, o_init)
+    fc.assert_parity(out, ref, fc.active_index(wl, rows), wl.name)
+    fc.assert_pads_untouched(out, o_init, wl, wl.name)
+
+    wl = Workload("rc_narrow", 7, 4096, 64, True, 0.125, (("normal", 0.0, 1.0),) * 3, seed=46)
+    q, k, v = wl.make_inputs()
+    o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
+    gx = (wl.seq_len + 15) // 16 - 3  # 253 x 7 = 1771 workgroups, above the coarse threshold
+    bufs = [nc.DeviceBuffer.from_array(x) for x in (q, k, v, o_init)]
+    try:
+        params = [ctypes.c_void_p(b.ptr) for b in bufs] + [
+            ctypes.c_uint64(wl.seq_len), ctypes.c_uint64(64), ctypes.c_uint64(wl.stride("q")),
+            ctypes.c_uint64(wl.stride("k")), ctypes.c_uint64(wl.stride("v")), ctypes.c_uint64(wl.stride("o")),
+            ctypes.c_float(wl.scale), ctypes.c_uint32(1)]
+        gpu.get_function("flash_attention_fwd_h64_bn32").launch((gx, wl.batch_heads), (128,), params)
+        nc.synchronize()
+        out = bufs[3].download(np.float32, wl.length("o"))
+    finally:
+        for b in bufs:
+            b.free()
+    # blocks 0 .. gx-1 (taken last-first by the causal body) cover rows 0 .. 16*gx-1
+    covered = np.arange(0, 16 * gx)
+    rows = np.unique(np.concatenate([covered[::97], [16 * gx - 1]]))
+    ref = fc.oracle(wl, q, k, v, rows=rows, o_init=o_init)
+    fc.assert_parity(out, ref, fc.active_index(wl, rows), "narrow grid")
+    untouched = fc.active_index(wl, np.arange(16 * gx, wl.seq_len))
+    assert np.array_equal(out[untouched].view(np.uint32), o_init[untouched].view(np.uint32))
