@@ -1412,22 +1412,26 @@ __device__ __forceinline__ void flash_fwd_pipe_kernel(const nc_flash_kernel_args
 // waves' partials merge through LDS. Lane l holds query l%16; in S^T tile t it holds keys 16t+4(l/16)+r,
 // and those 8 keys are, in order, its k-values of the P^T and V^T operands.
 // ---------------------------------------------------------------------------------------------
-constexpr int kRefMaxWaves = 4;
-
-// LDS of the reference-ABI body: per wave, one staged 32-key chunk of K and of V (rows padded to
-// D + 8 halves: the K reads of 16 rows at one column chunk and the transposed V reads then spread
-// over the banks), reused after the key loop for the waves' merge.
-template <int D>
+// LDS of the reference-ABI body: WAVES staging regions, each one staged 32-key chunk of K and of V
+// (rows padded to D + 8 halves: the K reads of 16 rows at one column chunk and the transposed V
+// reads then spread over the banks), reused after the key loop for the waves' merge. A launch of
+// NW waves runs two chunk streams per wave when 2 NW regions exist, else one (NW regions).
+template <int D, int WAVES>
 struct RefCfg {
     static constexpr int KP = D + 8;                 // staged row pitch, halves
     static constexpr int CHUNK = 32 * KP * 2;        // bytes of one staged K (or V) chunk
     static constexpr int WAVE = 2 * CHUNK;
     static constexpr int OP = D + 4;                 // merge row pitch, floats
-    static constexpr int MERGE = kRefMaxWaves * 16 * (8 + OP * 4);
-    static constexpr int LDS = kRefMaxWaves * WAVE > MERGE ? kRefMaxWaves * WAVE : MERGE;
+    static constexpr int MERGE = WAVES * 16 * (8 + OP * 4);
+    static constexpr int LDS = WAVES * WAVE > MERGE ? WAVES * WAVE : MERGE;
     static constexpr int SEG = 32 * (D / 8) / 64;    // 16-byte segments of a chunk per lane
 };
-constexpr int kRefLds = RefCfg<64>::LDS;
+// A symbol's LDS (d = 64 needs the most). The symbols the reference launches with 128 threads
+// hold four regions (two waves, two streams each); those it launches with 64 threads hold two (one
+// wave, two streams), so eight of their one-wave workgroups fit a CU instead of four, and accept at
+// most two waves.
+template <int WAVES>
+constexpr int ref_lds_bytes() { return RefCfg<64, WAVES>::LDS; }
 // Grid size (workgroups) from which the 128-thread d=64 launches take four 16-row blocks per
 // working workgroup (flash_fwd_refabi). Measured on MI355X with the reference's grid: from 1536
 // workgroups (384 working ones) it was 1.13-2.1x faster on every shape tried; at 1024 it was
@@ -1443,12 +1447,12 @@ constexpr uint64_t kRefCoarseMinWorkgroups = NC_REF_COARSE_MIN_WORKGROUPS;
 // K rows by ds_read_b128, V^T by ds_read_b64_tr_b16 (lane m of a 16-lane group supplies
 // V[r0 + m/4][d0 + 4(m%4)], lane i receives V[r0..r0+3][d0 + i]). Otherwise every operand element
 // is gathered from global memory (any stride, any base alignment).
-template <int D, bool VEC>
+template <int D, bool VEC, int WAVES>
 __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                                                       float *o, int S, uint64_t q_stride, uint64_t k_stride,
                                                       uint64_t v_stride, uint64_t o_stride, float scale,
                                                       bool causal, char *smem) {
-    using RC = RefCfg<D>;
+    using RC = RefCfg<D, WAVES>;
     constexpr int DH = (D + 31) / 32;  // 32-column k-steps of S^T
     constexpr int DT = D / 16;         // 16-row O^T tiles
     constexpr int OP = RC::OP;
@@ -1510,15 +1514,15 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
             *reinterpret_cast<NC_LDS(u32x4) *>((uintptr_t)(vst + off)) = vreg[j];
         }
     };
-    // Two chunk streams per wave (VEC, at most two waves: the reference's 64- and 128-thread
-    // launches, on slices that fit 32-bit buffer offsets). One wave per SIMD has nothing else to hide
+    // Two chunk streams per wave (VEC, two staging regions per wave: the reference's 64- and
+    // 128-thread launches, on slices that fit 32-bit buffer offsets). One wave per SIMD has nothing else to hide
     // a chunk's serial chain of LDS round trips, MFMAs and cross-lane reductions, so each wave keeps
     // two online-softmax states, A over its chunks w, w + 2NW, ... and B over w + NW, w + 3NW, ...,
     // runs the two chains side by side in one branch-free body and merges them after the loop. Each
     // stream stages in its own region (the two regions of a wave are the ones two more waves would
     // use), and the next pair's rows are fetched by range-checked buffer loads, which read zero past
     // the slice.
-    const bool pair = VEC && NW <= 2 && (uint64_t)S * D * 2 < (1ull << 31);
+    const bool pair = VEC && 2 * NW <= WAVES && (uint64_t)S * D * 2 < (1ull << 31);
     if (VEC && !pair && w < nch) fetch(w);
 
     const float sc = scale * kLog2e;
@@ -1746,7 +1750,7 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
     lt += __shfl_xor(lt, 32);
     __syncthreads();
     float2v *mlb = reinterpret_cast<float2v *>(smem);                                  // [NW][16]
-    float *ob = reinterpret_cast<float *>(smem + kRefMaxWaves * 16 * sizeof(float2v));  // [NW][16][OP]
+    float *ob = reinterpret_cast<float *>(smem + WAVES * 16 * sizeof(float2v));  // [NW][16][OP]
     if (g == 0) mlb[w * 16 + c] = float2v{mrow, lt};
     __syncthreads();
     float mmax = neg_inf(), den = 0.f;
@@ -1774,22 +1778,23 @@ __device__ __forceinline__ void flash_fwd_refabi_body(const uint16_t *q, const u
 //   D64_ONLY       head_dim != 64 returns without writing (src/flash_h64.zig:35,
 //                  src/flash_h64_bn32.zig:40, src/flash_h64_causal.zig:35); the other symbols accept
 //                  head_dim 16, 32 and 64 (src/flash_v2.zig:37, src/flash_opt.zig:31, src/kernels.zig:394).
-template <bool ALWAYS_CAUSAL, bool D64_ONLY>
+template <bool ALWAYS_CAUSAL, bool D64_ONLY, int WAVES>
 __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o,
                                                  uint64_t seq_len, uint64_t head_dim, uint64_t q_stride,
                                                  uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, float scale,
                                                  uint32_t causal) {
-    __shared__ __attribute__((aligned(16))) char smem[kRefLds];
-    // Shapes the reference's kernels reject return without writing (src/flash_h64_bn32.zig:40).
-    if (seq_len == 0 || seq_len > 0x7fffffffull || (blockDim.x & 63) || blockDim.x > 64 * kRefMaxWaves) return;
+    __shared__ __attribute__((aligned(16))) char smem[ref_lds_bytes<WAVES>()];
+    // Shapes the reference's kernels reject return without writing (src/flash_h64_bn32.zig:40), and
+    // launches of more waves than the symbol's LDS stages.
+    if (seq_len == 0 || seq_len > 0x7fffffffull || (blockDim.x & 63) || blockDim.x > 64u * WAVES) return;
     const int S = (int)seq_len;
     const bool cz = ALWAYS_CAUSAL || causal != 0;
     // 16-byte vector path when every slice base is 16-byte aligned (rows of head_dim halves are).
     const bool vec = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                        reinterpret_cast<uintptr_t>(v)) & 15u) == 0 && ((q_stride | k_stride | v_stride) & 7u) == 0;
     auto run = [&](auto dc, auto vc) {
-        flash_fwd_refabi_body<decltype(dc)::value, decltype(vc)::value != 0>(q, k, v, o, S, q_stride, k_stride, v_stride,
-                                                                              o_stride, scale, cz, smem);
+        flash_fwd_refabi_body<decltype(dc)::value, decltype(vc)::value != 0, WAVES>(q, k, v, o, S, q_stride, k_stride,
+                                                                                     v_stride, o_stride, scale, cz, smem);
     };
     // Large d=64 grids of two-wave workgroups (the reference's 128-thread launches): one workgroup
     // of each group of four consecutive 16-row blocks computes the group's 64 rows with the
@@ -1798,10 +1803,10 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
     // works rotates with the group and the slice, so the working ones spread over the XCDs. Only
     // for a grid of exactly ceil(S/16) blocks per slice (so no row outside the launch is written)
     // and 16-byte aligned Q/K/V/O slices (the pipelined body's float4 O stores).
+    constexpr bool COARSE = pipe_lds_bytes<64, 2, 1, 2, 2, false>() <= ref_lds_bytes<WAVES>();  // the body fits
     const bool o_vec = (reinterpret_cast<uintptr_t>(o) & 15u) == 0 && (o_stride & 3u) == 0;
-    if (head_dim == 64 && vec && o_vec && blockDim.x == 128 && gridDim.x == (seq_len + 15) / 16 &&
+    if (COARSE && head_dim == 64 && vec && o_vec && blockDim.x == 128 && gridDim.x == (seq_len + 15) / 16 &&
         (uint64_t)gridDim.x * gridDim.y >= kRefCoarseMinWorkgroups) {
-        static_assert(pipe_lds_bytes<64, 2, 1, 2, 2, false>() <= kRefLds, "the pipelined body fits the LDS");
         const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 2;
         const uint32_t sz = gx - 4u * m < 4u ? gx - 4u * m : 4u;
         if (bx != 4u * m + (by + m) % sz) return;
@@ -1991,17 +1996,20 @@ NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p1_causal, 16, 1, 8, true, 1, 1)
 // src/flash_h64_bn32.zig:26, src/flash_h64_causal.zig:20, src/kernels.zig:380): one body, launched
 // with the reference's grid (ceil(S/16), batch_heads) and 64 or 128 threads; each symbol keeps its
 // reference kernel's head_dim domain and causal handling (flash_fwd_refabi's two switches).
-#define NC_FLASH_REFABI_KERNEL(NAME, ALWAYS_CAUSAL, D64_ONLY)                                         \
+// WAVES: staging regions of the symbol's LDS, 4 for the symbols the reference launches with 128
+// threads and 2 for those it launches with 64 (src/flash.zig:84-95); a launch may use at most
+// WAVES waves.
+#define NC_FLASH_REFABI_KERNEL(NAME, ALWAYS_CAUSAL, D64_ONLY, WAVES)                                  \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                           \
         const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t seq_len,          \
         uint64_t head_dim, uint64_t q_stride, uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, \
         float scale, uint32_t causal) {                                                               \
-        flash_fwd_refabi<ALWAYS_CAUSAL, D64_ONLY>(q, k, v, o, seq_len, head_dim, q_stride, k_stride, v_stride, \
-                                                  o_stride, scale, causal);                          \
+        flash_fwd_refabi<ALWAYS_CAUSAL, D64_ONLY, WAVES>(q, k, v, o, seq_len, head_dim, q_stride, k_stride, \
+                                                         v_stride, o_stride, scale, causal);         \
     }
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_v2, false, false)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_opt, false, false)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64, false, true)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_bn32, false, true)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_causal, true, true)
-NC_FLASH_REFABI_KERNEL(flash_attention_fwd, false, false)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_v2, false, false, 4)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_opt, false, false, 2)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64, false, true, 2)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_bn32, false, true, 4)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd_h64_causal, true, true, 2)
+NC_FLASH_REFABI_KERNEL(flash_attention_fwd, false, false, 2)

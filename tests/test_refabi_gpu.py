@@ -184,3 +184,23 @@ def test_reference_symbol_large_grid_fallbacks(gpu):
     fc.assert_parity(out, ref, fc.active_index(wl, rows), "narrow grid")
     untouched = fc.active_index(wl, np.arange(16 * gx, wl.seq_len))
     assert np.array_equal(out[untouched].view(np.uint32), o_init[untouched].view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["flash_attention_fwd_opt", "flash_attention_fwd_h64", "flash_attention_fwd_h64_causal",
+                                  "flash_attention_fwd"])
+def test_reference_64_thread_symbols_stage_two_waves(gpu, name):
+    """The symbols the reference launches with 64 threads hold LDS for two waves: a 128-thread launch
+    (one chunk stream per wave) gives the 64-thread result, and a wider one writes nothing."""
+    wl = Workload("ra_w2", 3, 333, 64, name == "flash_attention_fwd_h64_causal", 0.125, (("normal", 0.0, 1.0),) * 3,
+                  seed=47)
+    q, k, v = wl.make_inputs()
+    o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
+    ref = fc.oracle(wl, q, k, v, o_init=o_init)
+    for threads in (64, 128):
+        print(f"[case] {name} threads={threads}", flush=True)
+        out = launch_reference_way(gpu, name, threads, wl, q, k, v, o_init)
+        fc.assert_parity(out, ref, fc.active_index(wl), f"{name}/{threads}")
+        fc.assert_pads_untouched(out, o_init, wl, f"{name}/{threads}")
+    print(f"[case] {name} threads=192", flush=True)
+    out = launch_reference_way(gpu, name, 192, wl, q, k, v, o_init)
+    assert np.array_equal(out.view(np.uint32), o_init.view(np.uint32)), name
