@@ -1441,6 +1441,7 @@ constexpr int ref_lds_bytes() { return RefCfg<64, WAVES>::LDS; }
 #endif
 constexpr uint64_t kRefCoarseMinWorkgroups = NC_REF_COARSE_MIN_WORKGROUPS;
 
+
 // VEC: every Q/K/V slice base is 16-byte aligned (pointers and slice strides; rows of D halves
 // are), so each wave loads a key chunk as one contiguous run of 16-byte segments, stages it in its
 // own LDS region (the next chunk's loads in flight meanwhile) and reads the MFMA operands there:
@@ -1835,14 +1836,54 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
             flash_fwd_pipe_body<64, 2, 1, false, 2, 2, false>(a, smem, slot);
         return;
     }
+    // One-wave workgroups (the reference's 64-thread launches): one workgroup of each pair of
+    // consecutive 16-row blocks computes both with the pipelined body (one 32-row wave, private
+    // two-stage staging), the other returns; the working one alternates with the pair and the slice.
+    // Same layout conditions as the four-block form above. Measured on MI355X against the 16-row
+    // body with the reference's grid: 1.5-2.2x faster from 1024 workgroups, 3-27 % faster on
+    // smaller grids, but 2-7 % slower on causal launches over few slices and long sequences (d=32
+    // BH=2-4, S=1024-2048: half the waves then carry the heavy blocks), which keep the 16-row body.
+    const bool pair_coarse = vec && o_vec && blockDim.x == 64 && gridDim.x == (seq_len + 15) / 16 &&
+                             (!cz || gridDim.y >= 8 || (uint64_t)gridDim.x * gridDim.y >= 512);
+    auto run_pairs = [&](auto dc) {
+        constexpr int DD = decltype(dc)::value;
+        static_assert(pipe_lds_bytes<DD, 1, 1, 2, 1, false>() <= ref_lds_bytes<2>(), "the pipelined body fits the LDS");
+        const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 1;
+        const uint32_t sz = gx - 2u * m < 2u ? gx - 2u * m : 2u;
+        if (bx != 2u * m + (by + m) % sz) return;
+        nc_flash_kernel_args a = {};
+        a.q = q;
+        a.k = k;
+        a.v = v;
+        a.o = o;
+        a.seq_len = seq_len;
+        a.head_dim = DD;
+        a.q_stride = q_stride;
+        a.k_stride = k_stride;
+        a.v_stride = v_stride;
+        a.o_stride = o_stride;
+        a.scale = scale;
+        a.causal = cz ? 1u : 0u;
+        a.q_row_stride = a.k_row_stride = a.v_row_stride = a.o_row_stride = DD;
+        a.batch_heads = gridDim.y;
+        a.num_q_blocks = (uint32_t)((seq_len + 31) / 32);
+        auto slot = [&](uint32_t) { return PipeSlot{0u, by, m}; };
+        if (cz)
+            flash_fwd_pipe_body<DD, 1, 1, true, 2, 1, false>(a, smem, slot);
+        else
+            flash_fwd_pipe_body<DD, 1, 1, false, 2, 1, false>(a, smem, slot);
+    };
     if (head_dim == 64) {
-        if (vec) run(IC<64>{}, IC<1>{}); else run(IC<64>{}, IC<0>{});
+        if (pair_coarse) run_pairs(IC<64>{});
+        else if (vec) run(IC<64>{}, IC<1>{}); else run(IC<64>{}, IC<0>{});
     } else if (D64_ONLY) {
         return;
     } else if (head_dim == 16) {
-        if (vec) run(IC<16>{}, IC<1>{}); else run(IC<16>{}, IC<0>{});
+        if (pair_coarse) run_pairs(IC<16>{});
+        else if (vec) run(IC<16>{}, IC<1>{}); else run(IC<16>{}, IC<0>{});
     } else if (head_dim == 32) {
-        if (vec) run(IC<32>{}, IC<1>{}); else run(IC<32>{}, IC<0>{});
+        if (pair_coarse) run_pairs(IC<32>{});
+        else if (vec) run(IC<32>{}, IC<1>{}); else run(IC<32>{}, IC<0>{});
     }
 }
 

@@ -204,3 +204,33 @@ def test_reference_64_thread_symbols_stage_two_waves(gpu, name):
     print(f"[case] {name} threads=192", flush=True)
     out = launch_reference_way(gpu, name, 192, wl, q, k, v, o_init)
     assert np.array_equal(out.view(np.uint32), o_init.view(np.uint32)), name
+
+
+# One-wave launches that take the two-block form (one workgroup of each pair of 16-row blocks runs
+# the pipelined body): odd block counts leave a last pair of one block; causal launches take it with
+# 8 or more slices or from 512 workgroups.
+PAIR_CASES = [
+    Workload("rp_d16", 8, 1100, 16, False, 0.25, (("normal", 0.0, 1.0),) * 3, seed=51),
+    Workload("rp_d32_c", 8, 1040, 32, True, 1.0 / 32 ** 0.5, (("normal", 0.0, 1.0),) * 3, seed=52),
+    Workload("rp_d64", 5, 520, 64, False, -0.125, (("normal", 0.0, 1.0),) * 3, seed=53),
+    Workload("rp_d32_c2", 2, 4200, 32, True, 0.2, (("normal", 0.0, 2.0),) * 3, seed=54),
+]
+
+
+@pytest.mark.parametrize("name", ["flash_attention_fwd_opt", "flash_attention_fwd", "flash_attention_fwd_h64",
+                                  "flash_attention_fwd_h64_causal"])
+@pytest.mark.parametrize("wl", PAIR_CASES, ids=lambda w: w.name)
+def test_reference_symbol_two_block_form(gpu, name, wl):
+    print(f"[case] {name} threads=64 {wl.describe()}", flush=True)
+    q, k, v = wl.make_inputs()
+    o_init = np.full(wl.length("o"), fc.SENTINEL, dtype=np.float32)
+    if name in D64_ONLY and wl.head_dim != 64:
+        out = launch_reference_way(gpu, name, 64, wl, q, k, v, o_init)
+        assert np.array_equal(out.view(np.uint32), o_init.view(np.uint32)), name
+        return
+    eff = dataclasses.replace(wl, causal=True) if name in ALWAYS_CAUSAL else wl
+    rows = _sampled(eff, 7)
+    ref = fc.oracle(eff, q, k, v, rows=rows, o_init=o_init)
+    out = launch_reference_way(gpu, name, 64, wl, q, k, v, o_init)
+    fc.assert_parity(out, ref, fc.active_index(eff, rows), f"{name}/{wl.name}")
+    fc.assert_pads_untouched(out, o_init, eff, f"{name}/{wl.name}")
