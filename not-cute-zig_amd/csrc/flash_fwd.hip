@@ -1797,60 +1797,11 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
         flash_fwd_refabi_body<decltype(dc)::value, decltype(vc)::value != 0, WAVES>(q, k, v, o, S, q_stride, k_stride,
                                                                                      v_stride, o_stride, scale, cz, smem);
     };
-    // Large d=64 grids of two-wave workgroups (the reference's 128-thread launches): one workgroup
-    // of each group of four consecutive 16-row blocks computes the group's 64 rows with the
-    // pipelined body (two 32-row query waves sharing each staged K/V block), and the other three
-    // return. Each K/V byte staged then serves 64 queries instead of 16. Which workgroup of a group
-    // works rotates with the group and the slice, so the working ones spread over the XCDs. Only
-    // for a grid of exactly ceil(S/16) blocks per slice (so no row outside the launch is written)
-    // and 16-byte aligned Q/K/V/O slices (the pipelined body's float4 O stores).
-    constexpr bool COARSE = pipe_lds_bytes<64, 2, 1, 2, 2, false>() <= ref_lds_bytes<WAVES>();  // the body fits
-    const bool o_vec = (reinterpret_cast<uintptr_t>(o) & 15u) == 0 && (o_stride & 3u) == 0;
-    if (COARSE && head_dim == 64 && vec && o_vec && blockDim.x == 128 && gridDim.x == (seq_len + 15) / 16 &&
-        (uint64_t)gridDim.x * gridDim.y >= kRefCoarseMinWorkgroups) {
-        const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 2;
-        const uint32_t sz = gx - 4u * m < 4u ? gx - 4u * m : 4u;
-        if (bx != 4u * m + (by + m) % sz) return;
-        nc_flash_kernel_args a = {};
-        a.q = q;
-        a.k = k;
-        a.v = v;
-        a.o = o;
-        a.seq_len = seq_len;
-        a.head_dim = 64;
-        a.q_stride = q_stride;
-        a.k_stride = k_stride;
-        a.v_stride = v_stride;
-        a.o_stride = o_stride;
-        a.scale = scale;
-        a.causal = cz ? 1u : 0u;
-        a.q_row_stride = a.k_row_stride = a.v_row_stride = a.o_row_stride = 64;
-        a.batch_heads = gridDim.y;
-        a.num_q_blocks = (uint32_t)((seq_len + 63) / 64);
-        // group m computes 64-row block m; causal blocks come heaviest first, as in the
-        // 16-row body, since qb_rev counts from the last block
-        auto slot = [&](uint32_t) { return PipeSlot{0u, by, m}; };
-        if (cz)
-            flash_fwd_pipe_body<64, 2, 1, true, 2, 2, false>(a, smem, slot);
-        else
-            flash_fwd_pipe_body<64, 2, 1, false, 2, 2, false>(a, smem, slot);
-        return;
-    }
-    // One-wave workgroups (the reference's 64-thread launches): one workgroup of each pair of
-    // consecutive 16-row blocks computes both with the pipelined body (one 32-row wave, private
-    // two-stage staging), the other returns; the working one alternates with the pair and the slice.
-    // Same layout conditions as the four-block form above. Measured on MI355X against the 16-row
-    // body with the reference's grid: 1.5-2.2x faster from 1024 workgroups, 3-27 % faster on
-    // smaller grids, but 2-7 % slower on causal launches over few slices and long sequences (d=32
-    // BH=2-4, S=1024-2048: half the waves then carry the heavy blocks), which keep the 16-row body.
-    const bool pair_coarse = vec && o_vec && blockDim.x == 64 && gridDim.x == (seq_len + 15) / 16 &&
-                             (!cz || gridDim.y >= 8 || (uint64_t)gridDim.x * gridDim.y >= 512);
-    auto run_pairs = [&](auto dc) {
-        constexpr int DD = decltype(dc)::value;
-        static_assert(pipe_lds_bytes<DD, 1, 1, 2, 1, false>() <= ref_lds_bytes<2>(), "the pipelined body fits the LDS");
-        const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 1;
-        const uint32_t sz = gx - 2u * m < 2u ? gx - 2u * m : 2u;
-        if (bx != 2u * m + (by + m) % sz) return;
+    // The pipelined body for `nqb` row blocks of BM rows: its argument block (rows of head_dim
+    // elements; no scratch, no balancing) and slot (block m of slice blockIdx.y; causal blocks come
+    // heaviest first, as in the 16-row body, since qb_rev counts from the last block).
+    auto pipe_run = [&](auto dc, auto nq_c, auto sub_c, uint32_t m) {
+        constexpr int DD = decltype(dc)::value, NQ = decltype(nq_c)::value, SUB = decltype(sub_c)::value;
         nc_flash_kernel_args a = {};
         a.q = q;
         a.k = k;
@@ -1866,12 +1817,48 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
         a.causal = cz ? 1u : 0u;
         a.q_row_stride = a.k_row_stride = a.v_row_stride = a.o_row_stride = DD;
         a.batch_heads = gridDim.y;
-        a.num_q_blocks = (uint32_t)((seq_len + 31) / 32);
-        auto slot = [&](uint32_t) { return PipeSlot{0u, by, m}; };
+        a.num_q_blocks = (uint32_t)((seq_len + 32 * NQ - 1) / (32 * NQ));
+        const uint32_t head = blockIdx.y;
+        auto slot = [&](uint32_t) { return PipeSlot{0u, head, m}; };
         if (cz)
-            flash_fwd_pipe_body<DD, 1, 1, true, 2, 1, false>(a, smem, slot);
+            flash_fwd_pipe_body<DD, NQ, 1, true, 2, SUB, false>(a, smem, slot);
         else
-            flash_fwd_pipe_body<DD, 1, 1, false, 2, 1, false>(a, smem, slot);
+            flash_fwd_pipe_body<DD, NQ, 1, false, 2, SUB, false>(a, smem, slot);
+    };
+    // Layout the pipelined body needs: 16-byte aligned Q/K/V slices, float4-aligned O slices (its O
+    // stores), slices within its 32-bit buffer offsets (up to one block past seq_len), and a grid of
+    // exactly ceil(S/16) blocks per slice, so that no row outside the launch is written.
+    const bool o_vec = (reinterpret_cast<uintptr_t>(o) & 15u) == 0 && (o_stride & 3u) == 0;
+    const bool pipe_ok = vec && o_vec && (seq_len + 512) * head_dim * 2 < (1ull << 31) &&
+                         gridDim.x == (seq_len + 15) / 16;
+    // Large d=64 grids of two-wave workgroups (the reference's 128-thread launches): one workgroup
+    // of each group of four consecutive 16-row blocks computes the group's 64 rows with the
+    // pipelined body (two 32-row query waves sharing each staged K/V block), and the other three
+    // return. Each K/V byte staged then serves 64 queries instead of 16. Which workgroup of a group
+    // works rotates with the group and the slice, so the working ones spread over the XCDs.
+    constexpr bool COARSE = pipe_lds_bytes<64, 2, 1, 2, 2, false>() <= ref_lds_bytes<WAVES>();  // the body fits
+    if (COARSE && pipe_ok && head_dim == 64 && blockDim.x == 128 &&
+        (uint64_t)gridDim.x * gridDim.y >= kRefCoarseMinWorkgroups) {
+        const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 2;
+        const uint32_t sz = gx - 4u * m < 4u ? gx - 4u * m : 4u;
+        if (bx == 4u * m + (by + m) % sz) pipe_run(IC<64>{}, IC<2>{}, IC<2>{}, m);
+        return;
+    }
+    // One-wave workgroups (the reference's 64-thread launches): one workgroup of each pair of
+    // consecutive 16-row blocks computes both with the pipelined body (one 32-row wave, private
+    // two-stage staging), the other returns; the working one alternates with the pair and the slice.
+    // Measured on MI355X against the 16-row body with the reference's grid: 1.5-2.2x faster from
+    // 1024 workgroups, 3-27 % faster on smaller grids, but 2-7 % slower on causal launches over few
+    // slices and long sequences (d=32 BH=2-4, S=1024-2048: half the waves then carry the heavy
+    // blocks), which keep the 16-row body.
+    const bool pair_coarse = pipe_ok && blockDim.x == 64 &&
+                             (!cz || gridDim.y >= 8 || (uint64_t)gridDim.x * gridDim.y >= 512);
+    auto run_pairs = [&](auto dc) {
+        static_assert(pipe_lds_bytes<decltype(dc)::value, 1, 1, 2, 1, false>() <= ref_lds_bytes<2>(),
+                      "the pipelined body fits the LDS");
+        const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 1;
+        const uint32_t sz = gx - 2u * m < 2u ? gx - 2u * m : 2u;
+        if (bx == 2u * m + (by + m) % sz) pipe_run(dc, IC<1>{}, IC<1>{}, m);
     };
     if (head_dim == 64) {
         if (pair_coarse) run_pairs(IC<64>{});
