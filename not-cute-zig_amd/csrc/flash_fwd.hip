@@ -622,7 +622,7 @@ struct PipeCfg {
     static constexpr int ML_OFF = RING > O_BYTES ? RING : O_BYTES;
     static constexpr bool QLDS = NS > 1;                                   // Q staged once in LDS
     static constexpr int QLOADS = BM * CH / 64;                            // its wave-instructions
-    static_assert(!QLDS || QLOADS <= NW, "one Q load per wave at most");
+    static_assert(!QLDS || QLOADS <= NW || QLOADS % NW == 0, "the waves share the Q loads evenly");
     static constexpr int Q_OFF = ML_OFF + NW * 32 * 2 * 4;
     static constexpr int LDS_BYTES = Q_OFF + (QLDS ? BM * D * 2 : 0);
     static constexpr int MT = D < 32 ? 1 : D / 32;
@@ -813,12 +813,18 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
                                                      16, (uint32_t)(qb_tile * 32 + r) * qrb + (sl ^ SW::f(r)) * 16, 0, 0, 0);
         }
     } else if constexpr (C::QLDS) {
-        if (w < C::QLOADS) {
-            const __amdgpu_buffer_rsrc_t qrr = make_rsrc(a.q + (size_t)head * a.q_stride, qspan);
-            const int p = w * 64 + lane;
+        const __amdgpu_buffer_rsrc_t qrr = make_rsrc(a.q + (size_t)head * a.q_stride, qspan);
+        auto q_load = [&](int t) {  // wave-instruction t of the Q tile
+            const int p = t * 64 + lane;
             const int r = p / C::CH, sl = p % C::CH;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(qrr, (NC_LDS(void) *)(smem + C::Q_OFF + w * 1024), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(qrr, (NC_LDS(void) *)(smem + C::Q_OFF + t * 1024), 16,
                                                      (uint32_t)(q0 + r) * qrb + (sl ^ SW::f(r)) * 16, 0, 0, 0);
+        };
+        if constexpr (C::QLOADS <= C::NW) {
+            if (w < C::QLOADS) q_load(w);
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::QLOADS / C::NW; ++i) q_load(w + C::NW * i);
         }
     } else {
 #pragma unroll
@@ -1432,12 +1438,23 @@ struct RefCfg {
 // most two waves.
 template <int WAVES>
 constexpr int ref_lds_bytes() { return RefCfg<64, WAVES>::LDS; }
+// A symbol's LDS: its staging regions, or what the pipelined forms it may run need (the 128-thread
+// symbols: 32 rows over two key-split waves, or 64 rows over two query waves; the 64-thread ones:
+// 32 rows on one wave), whichever is more.
+template <int WAVES>
+constexpr int ref_symbol_lds_bytes() {
+    constexpr int pipe = WAVES >= 4 ? (pipe_lds_bytes<64, 1, 2, 2, 1, false>() > pipe_lds_bytes<64, 2, 1, 2, 2, false>()
+                                           ? pipe_lds_bytes<64, 1, 2, 2, 1, false>()
+                                           : pipe_lds_bytes<64, 2, 1, 2, 2, false>())
+                                    : pipe_lds_bytes<64, 1, 1, 2, 1, false>();
+    return ref_lds_bytes<WAVES>() > pipe ? ref_lds_bytes<WAVES>() : pipe;
+}
 // Grid size (workgroups) from which the 128-thread d=64 launches take four 16-row blocks per
-// working workgroup (flash_fwd_refabi). Measured on MI355X with the reference's grid: from 1536
-// workgroups (384 working ones) it was 1.13-2.1x faster on every shape tried; at 1024 it was
-// mixed (S=2048 faster, S=1024 10-15 % slower) and at 512-768 slower (c3 19.6 against 14.5 us).
+// working workgroup instead of two (flash_fwd_refabi). Measured on MI355X with the reference's
+// grid: the four-block form is 5.5 % faster on c5 (32768 workgroups: the L2 traffic binds), equal
+// on c4 (8192), and 10-37 % slower from 1536 to 4096 workgroups.
 #ifndef NC_REF_COARSE_MIN_WORKGROUPS
-#define NC_REF_COARSE_MIN_WORKGROUPS 1536
+#define NC_REF_COARSE_MIN_WORKGROUPS 16384
 #endif
 constexpr uint64_t kRefCoarseMinWorkgroups = NC_REF_COARSE_MIN_WORKGROUPS;
 
@@ -1784,7 +1801,7 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
                                                  uint64_t seq_len, uint64_t head_dim, uint64_t q_stride,
                                                  uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, float scale,
                                                  uint32_t causal) {
-    __shared__ __attribute__((aligned(16))) char smem[ref_lds_bytes<WAVES>()];
+    __shared__ __attribute__((aligned(16))) char smem[ref_symbol_lds_bytes<WAVES>()];
     // Shapes the reference's kernels reject return without writing (src/flash_h64_bn32.zig:40), and
     // launches of more waves than the symbol's LDS stages.
     if (seq_len == 0 || seq_len > 0x7fffffffull || (blockDim.x & 63) || blockDim.x > 64u * WAVES) return;
@@ -1800,8 +1817,9 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
     // The pipelined body for `nqb` row blocks of BM rows: its argument block (rows of head_dim
     // elements; no scratch, no balancing) and slot (block m of slice blockIdx.y; causal blocks come
     // heaviest first, as in the 16-row body, since qb_rev counts from the last block).
-    auto pipe_run = [&](auto dc, auto nq_c, auto sub_c, uint32_t m) {
-        constexpr int DD = decltype(dc)::value, NQ = decltype(nq_c)::value, SUB = decltype(sub_c)::value;
+    auto pipe_run = [&](auto dc, auto nq_c, auto ns_c, auto sub_c, uint32_t m) {
+        constexpr int DD = decltype(dc)::value, NQ = decltype(nq_c)::value, NS = decltype(ns_c)::value;
+        constexpr int SUB = decltype(sub_c)::value;
         nc_flash_kernel_args a = {};
         a.q = q;
         a.k = k;
@@ -1821,9 +1839,9 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
         const uint32_t head = blockIdx.y;
         auto slot = [&](uint32_t) { return PipeSlot{0u, head, m}; };
         if (cz)
-            flash_fwd_pipe_body<DD, NQ, 1, true, 2, SUB, false>(a, smem, slot);
+            flash_fwd_pipe_body<DD, NQ, NS, true, 2, SUB, false>(a, smem, slot);
         else
-            flash_fwd_pipe_body<DD, NQ, 1, false, 2, SUB, false>(a, smem, slot);
+            flash_fwd_pipe_body<DD, NQ, NS, false, 2, SUB, false>(a, smem, slot);
     };
     // Layout the pipelined body needs: 16-byte aligned Q/K/V slices, float4-aligned O slices (its O
     // stores), slices within its 32-bit buffer offsets (up to one block past seq_len), and a grid of
@@ -1831,17 +1849,17 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
     const bool o_vec = (reinterpret_cast<uintptr_t>(o) & 15u) == 0 && (o_stride & 3u) == 0;
     const bool pipe_ok = vec && o_vec && (seq_len + 512) * head_dim * 2 < (1ull << 31) &&
                          gridDim.x == (seq_len + 15) / 16;
-    // Large d=64 grids of two-wave workgroups (the reference's 128-thread launches): one workgroup
-    // of each group of four consecutive 16-row blocks computes the group's 64 rows with the
-    // pipelined body (two 32-row query waves sharing each staged K/V block), and the other three
+    // Very large d=64 grids of two-wave workgroups (the reference's 128-thread launches): one
+    // workgroup of each group of four consecutive 16-row blocks computes the group's 64 rows with
+    // the pipelined body (two 32-row query waves sharing each staged K/V block), and the other three
     // return. Each K/V byte staged then serves 64 queries instead of 16. Which workgroup of a group
     // works rotates with the group and the slice, so the working ones spread over the XCDs.
-    constexpr bool COARSE = pipe_lds_bytes<64, 2, 1, 2, 2, false>() <= ref_lds_bytes<WAVES>();  // the body fits
+    constexpr bool COARSE = WAVES >= 4;  // the two-wave pipelined forms (their LDS: ref_symbol_lds_bytes)
     if (COARSE && pipe_ok && head_dim == 64 && blockDim.x == 128 &&
         (uint64_t)gridDim.x * gridDim.y >= kRefCoarseMinWorkgroups) {
         const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 2;
         const uint32_t sz = gx - 4u * m < 4u ? gx - 4u * m : 4u;
-        if (bx == 4u * m + (by + m) % sz) pipe_run(IC<64>{}, IC<2>{}, IC<2>{}, m);
+        if (bx == 4u * m + (by + m) % sz) pipe_run(IC<64>{}, IC<2>{}, IC<1>{}, IC<2>{}, m);
         return;
     }
     // One-wave workgroups (the reference's 64-thread launches): one workgroup of each pair of
@@ -1854,22 +1872,35 @@ __device__ __forceinline__ void flash_fwd_refabi(const uint16_t *q, const uint16
     const bool pair_coarse = pipe_ok && blockDim.x == 64 &&
                              (!cz || gridDim.y >= 8 || (uint64_t)gridDim.x * gridDim.y >= 512);
     auto run_pairs = [&](auto dc) {
-        static_assert(pipe_lds_bytes<decltype(dc)::value, 1, 1, 2, 1, false>() <= ref_lds_bytes<2>(),
+        static_assert(pipe_lds_bytes<decltype(dc)::value, 1, 1, 2, 1, false>() <= ref_symbol_lds_bytes<2>(),
                       "the pipelined body fits the LDS");
         const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 1;
         const uint32_t sz = gx - 2u * m < 2u ? gx - 2u * m : 2u;
-        if (bx == 2u * m + (by + m) % sz) pipe_run(dc, IC<1>{}, IC<1>{}, m);
+        if (bx == 2u * m + (by + m) % sz) pipe_run(dc, IC<1>{}, IC<1>{}, IC<1>{}, m);
+    };
+    // Two-wave workgroups below the four-block form's grid size: one workgroup of each pair of
+    // 16-row blocks computes both (32 rows) with the pipelined body, its two waves splitting the
+    // keys. Measured on MI355X against the 16-row body with the reference's grid: 10-44 % faster on
+    // every shape tried (c3 14.6 -> 12.5 us, c1 3.16 -> 2.68 us, d=64 BH=4 S=4096 causal 57 -> 32 us).
+    const bool pair2 = COARSE && pipe_ok && blockDim.x == 128;
+    auto run_pairs2 = [&](auto dc) {
+        const uint32_t gx = gridDim.x, bx = blockIdx.x, by = blockIdx.y, m = bx >> 1;
+        const uint32_t sz = gx - 2u * m < 2u ? gx - 2u * m : 2u;
+        if (bx == 2u * m + (by + m) % sz) pipe_run(dc, IC<1>{}, IC<2>{}, IC<1>{}, m);
     };
     if (head_dim == 64) {
         if (pair_coarse) run_pairs(IC<64>{});
+        else if (pair2) run_pairs2(IC<64>{});
         else if (vec) run(IC<64>{}, IC<1>{}); else run(IC<64>{}, IC<0>{});
     } else if (D64_ONLY) {
         return;
     } else if (head_dim == 16) {
         if (pair_coarse) run_pairs(IC<16>{});
+        else if (pair2) run_pairs2(IC<16>{});
         else if (vec) run(IC<16>{}, IC<1>{}); else run(IC<16>{}, IC<0>{});
     } else if (head_dim == 32) {
         if (pair_coarse) run_pairs(IC<32>{});
+        else if (pair2) run_pairs2(IC<32>{});
         else if (vec) run(IC<32>{}, IC<1>{}); else run(IC<32>{}, IC<0>{});
     }
 }
