@@ -842,7 +842,7 @@ __device__ __forceinline__ void flash_fwd_pipe_body(const nc_flash_kernel_args &
     // the end of the grid (the step below). Workgroups before the balancing tail run above it
     // (priority 3), which keeps the arbiter's oldest-first order between them and the tail.
     constexpr bool BALANCE = !PRIV && !CAUSAL;
-    const bool balancing = BALANCE && a.balance_tail != 0u && L + a.balance_tail >= gridDim.x;
+    const bool balancing = BALANCE && a.balance_tail != 0u && (uint64_t)L + a.balance_tail >= gridDim.x;
     if (BALANCE && a.balance_tail != 0u && !balancing) __builtin_amdgcn_s_setprio(3);
     const int kv_end = CAUSAL ? min(S, q0 + C::BM) : S;
     int nblk = (kv_end + C::BN - 1) / C::BN;
