@@ -3,10 +3,10 @@
 
 One step = one flash-attention forward of the headline workload (BH=8 S=1024 d=64 causal, f16 in,
 f32 out) with Q/K/V already resident in HBM. Launches go through the C ABI (nc_flash_launch_async)
-on one stream; the timed region replays a HIP graph of back-to-back launches, bracketed by HIP
-events on that stream and a device synchronize on both sides, so the average per step is the
-kernel's average duration plus the (small) inter-kernel gap. Before it: --warmup untimed steps and
-a wall-clock settle phase (--settle-ms) of replays of the same graph, so that a short --warmup does
+on one stream; the timed region is one replay of a HIP graph that holds the K timed launches back to
+back between two HIP event-record nodes, with a device synchronize on both sides, so the average per
+step is the kernel's average duration plus the (small) inter-kernel gap. Before it: --warmup untimed
+steps and a wall-clock settle phase (--settle-ms) of graph replays, so that a short --warmup does
 not time a GPU that is still raising its clock.
 
 Prints ONE JSON line (rank 0, N=1) with the metric of the benchmark plan, a `roofline` object for
@@ -38,6 +38,7 @@ from flash_workloads import CONFIGS, HEADLINE  # noqa: E402
 PEAK_F16_TFLOPS = 2516.6  # 256 CU x 4096 flop/clk x 2.4 GHz, dense
 PEAK_HBM_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "flash_fwd_{workload}_traffic.txt")
+MAX_TIMED_NODES = 20000  # launches captured into the one timed graph
 
 
 def log(msg: str) -> None:
@@ -117,56 +118,64 @@ def calibrate_copy(mod: nc.Module, stream: nc.Stream, nbytes: int, iters: int) -
 
 
 def time_graph(stream, launch, steps: int, warmup: int, graph_batch: int, settle_ms: float) -> dict:
-    """Time exactly `steps` launches issued as replays of a HIP graph of back-to-back launches,
-    between HIP events on the launch stream with a device synchronize on both sides.
+    """Time exactly `steps` launches, back to back on the GPU, with a device synchronize on both sides.
 
-    Before the timed region: `warmup` untimed steps as replays of the same graph, then a clock-settle
-    phase that keeps replaying it until `settle_ms` of wall time have passed (a GPU that has idled
-    runs its first milliseconds of work on a lower clock, and a short --warmup alone would time
-    that). At most 10 graphs are queued between synchronizes: under rocprofv3's kernel tracer, about
-    200 queued graphs of 100 launches each made the host runtime abort."""
+    The timed graph holds two untimed launches, a HIP event-record node, the `steps` launches and a
+    second record node, so the event pair brackets exactly those launches, issued as the GPU runs a
+    graph: neither the host's submission nor the graph's own launch cost (~7.7 us per replay on
+    MI355X, measured as the difference between events around a replay and record nodes inside it:
+    ~0.38 us of every step at 20 steps) falls between the two records. The untimed launches keep the
+    GPU busy from the replay's start to the first record.
+
+    Before the measured replay: `warmup` untimed steps as replays of a graph of up to `graph_batch`
+    launches, one untimed replay of the timed graph (a new graph's first replay carries one-time
+    set-up), then a clock-settle phase that keeps replaying the timed graph until `settle_ms` of wall
+    time have passed (a GPU that has idled runs its first milliseconds of work on a lower clock, and
+    a short --warmup alone would time that). At most 10 graphs are queued between synchronizes:
+    under rocprofv3's kernel tracer, about 200 queued graphs of 100 launches each made the host
+    runtime abort."""
+    if steps > MAX_TIMED_NODES:
+        raise ValueError(f"--steps {steps}: at most {MAX_TIMED_NODES} launches are timed in one graph")
     gb = max(1, min(graph_batch, steps))
-    full, rest = divmod(steps, gb)
     graph = nc.Graph.capture(stream, lambda: [launch() for _ in range(gb)])
-    tail = nc.Graph.capture(stream, lambda: [launch() for _ in range(rest)]) if rest else None
+    # Timing-only events: their records skip the system-scope cache flush of a default event, which
+    # would otherwise sit inside the event pair ahead of the first timed kernel.
+    ev0, ev1 = nc.Event(timing_only=True), nc.Event(timing_only=True)
+
+    def timed_body():
+        launch()
+        launch()
+        ev0.record_node(stream.handle)
+        for _ in range(steps):
+            launch()
+        ev1.record_node(stream.handle)
+
+    timed = nc.Graph.capture(stream, timed_body)
     for i in range(warmup // gb):
         graph.launch(stream)
         if i % 10 == 9:
             stream.synchronize()
+    timed.launch(stream)
     stream.synchronize()
     t0 = time.perf_counter()
     settle_graphs = 0
     while (time.perf_counter() - t0) * 1e3 < settle_ms:
-        for _ in range(10):
-            graph.launch(stream)
-        settle_graphs += 10
+        for _ in range(max(1, min(10, 100 // steps))):
+            timed.launch(stream)
+            settle_graphs += 1
         stream.synchronize()
     settled = (time.perf_counter() - t0) * 1e3
-    # Timing-only events: their records skip the system-scope cache flush of a default event, which
-    # would otherwise sit inside the event pair ahead of the first timed kernel.
-    ev0, ev1 = nc.Event(timing_only=True), nc.Event(timing_only=True)
     nc.synchronize()
-    # Two untimed replays queued ahead of the start event keep the GPU busy while the host submits
-    # the timed graphs, so the event pair brackets the K launches themselves rather than the host's
-    # submission latency of the first timed graph (with K = 20 that was ~1.5 us of every step).
-    graph.launch(stream)
-    graph.launch(stream)
-    ev0.record(stream.handle)
-    for i in range(full):
-        graph.launch(stream)
-    if tail is not None:
-        tail.launch(stream)
-    ev1.record(stream.handle)
-    ev1.synchronize()
+    timed.launch(stream)
+    stream.synchronize()
     nc.synchronize()
     total_ms = nc.Event.elapsed(ev0, ev1)
     graph.destroy()
-    if tail is not None:
-        tail.destroy()
+    timed.destroy()
     ev0.destroy()
     ev1.destroy()
     return {"ms_per_step": total_ms / steps, "total_ms": total_ms, "steps": steps,
-            "settle_ms": round(settled, 1), "settle_launches": settle_graphs * gb}
+            "settle_ms": round(settled, 1), "settle_launches": settle_graphs * (steps + 2)}
 
 
 def measure_mfma_ceiling(mod, stream, budget_ms: float, ops16) -> dict:
@@ -455,8 +464,9 @@ def main() -> int:
         "flops_per_step": work["flops"],
         "flops_per_step_reference_formula": work["flops_reference"],
         "bytes_per_step": work["bytes"],
-        "timing": "HIP events around graph replays of back-to-back launches on the launch stream, after "
-                  "--warmup replays and a wall-clock settle phase of replays",
+        "timing": "HIP event-record nodes inside one captured graph around exactly the timed back-to-back "
+                  "launches (after two untimed ones), device synchronize before and after its replay; before "
+                  "it --warmup steps and a wall-clock settle phase of replays of the same graph",
         "settle_ms": t["settle_ms"],
         "settle_launches": t["settle_launches"],
         "per_launch_event_ms": {"mean": per_launch.mean_ms, "min": per_launch.min_ms, "max": per_launch.max_ms,

@@ -163,6 +163,11 @@ int nc_event_create(nc_event *out);
 int nc_event_create_timing(nc_event *out);
 int nc_event_destroy(nc_event ev);
 int nc_event_record(nc_event ev, nc_stream stream);
+/* Extension: record `ev` on `stream` as a node of the graph being captured there (hipEventRecordExternal;
+ * outside a capture, the same as nc_event_record). Each replay of the graph records the event at that
+ * point of the graph, so a pair of such nodes times the launches between them without the graph's
+ * own launch cost. */
+int nc_event_record_node(nc_event ev, nc_stream stream);
 int nc_event_synchronize(nc_event ev);
 int nc_event_elapsed(float *ms, nc_event start, nc_event stop);
 

@@ -394,6 +394,11 @@ int nc_event_record(nc_event ev, nc_stream stream) {
     return check(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream), "hipEventRecord");
 }
 
+int nc_event_record_node(nc_event ev, nc_stream stream) {
+    return check(hipEventRecordWithFlags((hipEvent_t)ev, (hipStream_t)stream, hipEventRecordExternal),
+                 "hipEventRecordWithFlags(external)");
+}
+
 int nc_event_synchronize(nc_event ev) { return check(hipEventSynchronize((hipEvent_t)ev), "hipEventSynchronize"); }
 
 int nc_event_elapsed(float *ms, nc_event start, nc_event stop) {

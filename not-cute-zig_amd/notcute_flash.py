@@ -217,6 +217,7 @@ _SIGS = {
     "nc_event_create_timing": (ctypes.c_int, [ctypes.POINTER(_P)]),
     "nc_event_destroy": (ctypes.c_int, [_P]),
     "nc_event_record": (ctypes.c_int, [_P, _P]),
+    "nc_event_record_node": (ctypes.c_int, [_P, _P]),
     "nc_event_synchronize": (ctypes.c_int, [_P]),
     "nc_event_elapsed": (ctypes.c_int, [ctypes.POINTER(ctypes.c_float), _P, _P]),
     "nc_stream_begin_capture": (ctypes.c_int, [_P]),
@@ -548,6 +549,10 @@ class Event:
 
     def record(self, stream: Optional[int] = None) -> None:
         check(lib().nc_event_record(self.handle, stream), "Event.record")
+
+    def record_node(self, stream: Optional[int] = None) -> None:
+        """nc_event_record_node: under a stream capture, a record node of the captured graph."""
+        check(lib().nc_event_record_node(self.handle, stream), "Event.recordNode")
 
     def synchronize(self) -> None:
         check(lib().nc_event_synchronize(self.handle), "Event.synchronize")

@@ -69,3 +69,56 @@ def test_graph_replays_match_eager(gpu):
         stream.destroy()
         for buf in a + b + c:
             buf.free()
+
+
+def test_event_record_nodes_bracket_launches_inside_a_graph(gpu):
+    """nc_event_record_node during a capture puts the event records into the graph (bench.py times
+    its K launches this way): every replay records both events; the pair brackets only the launches
+    between them, so it measures less than an event pair recorded around the whole replay, which also
+    holds the two launches before the first node and the graph's own launch; and the launches inside
+    still compute the eager result."""
+    wl = Workload("graph_nodes", 8, 512, 64, True, 0.125, (("normal", 0.0, 1.0),) * 3, seed=44)
+    say(f"[case] record nodes around 10 launches of {wl.describe()}")
+    bufs = _device(wl)
+    stream = nc.Stream()
+    n0, n1 = nc.Event(timing_only=True), nc.Event(timing_only=True)
+    o0, o1 = nc.Event(timing_only=True), nc.Event(timing_only=True)
+    graph = None
+    try:
+        def launch():
+            nc.flash_launch(gpu, *bufs, wl.options(), stream=stream.handle)
+
+        launch()
+        stream.synchronize()
+        ref = bufs[3].download(np.float32, wl.length("o"))
+
+        def body():
+            launch()
+            launch()
+            n0.record_node(stream.handle)
+            for _ in range(10):
+                launch()
+            n1.record_node(stream.handle)
+
+        graph = nc.Graph.capture(stream, body)
+        for r in range(3):
+            bufs[3].memset(0)
+            nc.synchronize()
+            o0.record(stream.handle)
+            graph.launch(stream)
+            o1.record(stream.handle)
+            stream.synchronize()
+            inside, outside = nc.Event.elapsed(n0, n1), nc.Event.elapsed(o0, o1)
+            out = bufs[3].download(np.float32, wl.length("o"))
+            assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), f"replay {r}: output differs"
+            assert 0.0 < inside < outside, f"replay {r}: inside {inside} ms, outside {outside} ms"
+            say(f"[ok] replay {r}: 10 launches {inside * 1e3:.1f} us between the nodes, "
+                f"{outside * 1e3:.1f} us around the replay")
+    finally:
+        if graph is not None:
+            graph.destroy()
+        stream.destroy()
+        for e in (n0, n1, o0, o1):
+            e.destroy()
+        for buf in bufs:
+            buf.free()
