@@ -117,8 +117,11 @@ def calibrate_copy(mod: nc.Module, stream: nc.Stream, nbytes: int, iters: int) -
     log(f"calibration copy: {iters} x {n16 * 16} bytes read + written")
 
 
-def time_graph(stream, launch, steps: int, warmup: int, graph_batch: int, settle_ms: float) -> dict:
+def time_graph(stream, launch, steps: int, warmup: int, graph_batch: int, settle_ms: float,
+               method: str = "nodes") -> dict:
     """Time exactly `steps` launches, back to back on the GPU, with a device synchronize on both sides.
+    method "replays" times them as bench.py did before: events recorded on the stream around replays
+    of graphs of `graph_batch` launches (time_graph_replays).
 
     The timed graph holds two untimed launches, a HIP event-record node, the `steps` launches and a
     second record node, so the event pair brackets exactly those launches, issued as the GPU runs a
@@ -134,6 +137,8 @@ def time_graph(stream, launch, steps: int, warmup: int, graph_batch: int, settle
     a short --warmup alone would time that). At most 10 graphs are queued between synchronizes:
     under rocprofv3's kernel tracer, about 200 queued graphs of 100 launches each made the host
     runtime abort."""
+    if method == "replays":
+        return time_graph_replays(stream, launch, steps, warmup, graph_batch, settle_ms)
     if steps > MAX_TIMED_NODES:
         raise ValueError(f"--steps {steps}: at most {MAX_TIMED_NODES} launches are timed in one graph")
     gb = max(1, min(graph_batch, steps))
@@ -176,6 +181,52 @@ def time_graph(stream, launch, steps: int, warmup: int, graph_batch: int, settle
     ev1.destroy()
     return {"ms_per_step": total_ms / steps, "total_ms": total_ms, "steps": steps,
             "settle_ms": round(settled, 1), "settle_launches": settle_graphs * (steps + 2)}
+
+
+def time_graph_replays(stream, launch, steps: int, warmup: int, graph_batch: int, settle_ms: float) -> dict:
+    """Time exactly `steps` launches as replays of graphs of up to `graph_batch` back-to-back launches,
+    between HIP events recorded on the launch stream (so each graph's own launch cost, ~7.7 us, falls
+    inside the pair), with two untimed replays queued ahead of the first event and a device
+    synchronize on both sides; before them `warmup` steps and a clock-settle phase of replays. For
+    runs under rocprofv3's kernel tracer, which executes a graph holding event-record nodes node by
+    node (~67 us per launch on MI355X) but runs these graphs back to back."""
+    gb = max(1, min(graph_batch, steps))
+    full, rest = divmod(steps, gb)
+    graph = nc.Graph.capture(stream, lambda: [launch() for _ in range(gb)])
+    tail = nc.Graph.capture(stream, lambda: [launch() for _ in range(rest)]) if rest else None
+    for i in range(warmup // gb):
+        graph.launch(stream)
+        if i % 10 == 9:
+            stream.synchronize()
+    stream.synchronize()
+    t0 = time.perf_counter()
+    settle_graphs = 0
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        for _ in range(10):
+            graph.launch(stream)
+        settle_graphs += 10
+        stream.synchronize()
+    settled = (time.perf_counter() - t0) * 1e3
+    ev0, ev1 = nc.Event(timing_only=True), nc.Event(timing_only=True)
+    nc.synchronize()
+    graph.launch(stream)
+    graph.launch(stream)
+    ev0.record(stream.handle)
+    for _ in range(full):
+        graph.launch(stream)
+    if tail is not None:
+        tail.launch(stream)
+    ev1.record(stream.handle)
+    ev1.synchronize()
+    nc.synchronize()
+    total_ms = nc.Event.elapsed(ev0, ev1)
+    graph.destroy()
+    if tail is not None:
+        tail.destroy()
+    ev0.destroy()
+    ev1.destroy()
+    return {"ms_per_step": total_ms / steps, "total_ms": total_ms, "steps": steps,
+            "settle_ms": round(settled, 1), "settle_launches": settle_graphs * gb}
 
 
 def measure_mfma_ceiling(mod, stream, budget_ms: float, ops16) -> dict:
@@ -261,7 +312,7 @@ def measure_extra(mod, name: str, args) -> dict:
             bar_abs, bar_rel = flashcheck.parity_bar(wl.dtype)
             if not (max_abs <= bar_abs and max_rel <= bar_rel):
                 raise RuntimeError(f"{name}: parity failure max-abs {max_abs} max-rel {max_rel}")
-        t = time_graph(stream, launch, args.steps, args.warmup, args.graph_batch, args.settle_ms)
+        t = time_graph(stream, launch, args.steps, args.warmup, args.graph_batch, args.settle_ms, args.timing)
         tflops = work["flops"] / (t["ms_per_step"] * 1e-3) / 1e12
         gbps = work["bytes"] / (t["ms_per_step"] * 1e-3) / 1e9
         log(f"bench: {wl.describe()} -> {sel.name.decode()}: {t['ms_per_step'] * 1e3:.2f} us/step, "
@@ -292,6 +343,9 @@ def main() -> int:
                     help="untimed warmup steps: up to 50 eager launches, the rest graph replays")
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(CONFIGS))
     ap.add_argument("--graph-batch", type=int, default=100, help="launches captured per HIP graph")
+    ap.add_argument("--timing", choices=("nodes", "replays"), default="nodes",
+                    help="nodes: event-record nodes inside one graph around the timed launches; replays: events "
+                         "around replays of --graph-batch graphs (for runs under rocprofv3's kernel tracer)")
     ap.add_argument("--settle-ms", type=float, default=300.0,
                     help="untimed clock-settle replays of the timed graph, in wall-clock ms, after --warmup")
     ap.add_argument("--extra", default="c1,c2_causal,c2_full,c4,c5",
@@ -367,7 +421,8 @@ def main() -> int:
                                bytes_=work["bytes"], flops=work["flops_reference"], stream=stream.handle)
 
     # timed region: graphs of back-to-back launches
-    t = time_graph(stream, launch, args.steps, args.warmup - eager_warmup, args.graph_batch, args.settle_ms)
+    t = time_graph(stream, launch, args.steps, args.warmup - eager_warmup, args.graph_batch, args.settle_ms,
+                   args.timing)
     ms, steps = t["ms_per_step"], t["steps"]
     log(f"bench: {steps} steps in {t['total_ms']:.3f} ms -> {ms * 1e3:.3f} us/step (after {t['settle_ms']:.0f} ms "
         f"of clock-settle replays); per-launch event timing mean {per_launch.mean_ms * 1e3:.2f} us "
@@ -391,7 +446,7 @@ def main() -> int:
     # Fixed per-launch cost: an empty kernel with the same grid and block, replayed the same way.
     empty = mod.get_function("nc_util_empty")
     tf_ = time_graph(stream, lambda: empty.launch(tuple(sel.grid), (sel.threads,), [ka], stream=stream.handle),
-                     steps, 0, args.graph_batch, min(args.settle_ms, 50.0))
+                     steps, 0, args.graph_batch, min(args.settle_ms, 50.0), args.timing)
     floor_ms = tf_["ms_per_step"]
     log(f"bench: empty kernel with the same grid: {floor_ms * 1e3:.3f} us/launch")
 
@@ -464,9 +519,13 @@ def main() -> int:
         "flops_per_step": work["flops"],
         "flops_per_step_reference_formula": work["flops_reference"],
         "bytes_per_step": work["bytes"],
-        "timing": "HIP event-record nodes inside one captured graph around exactly the timed back-to-back "
-                  "launches (after two untimed ones), device synchronize before and after its replay; before "
-                  "it --warmup steps and a wall-clock settle phase of replays of the same graph",
+        "timing": ("HIP event-record nodes inside one captured graph around exactly the timed back-to-back "
+                   "launches (after two untimed ones), device synchronize before and after its replay; before "
+                   "it --warmup steps and a wall-clock settle phase of replays of the same graph")
+                  if args.timing == "nodes" else
+                  ("HIP events on the launch stream around replays of graphs of --graph-batch back-to-back "
+                   "launches (each graph's own launch cost inside the pair), after --warmup replays and a "
+                   "wall-clock settle phase of replays"),
         "settle_ms": t["settle_ms"],
         "settle_launches": t["settle_launches"],
         "per_launch_event_ms": {"mean": per_launch.mean_ms, "min": per_launch.min_ms, "max": per_launch.max_ms,
