@@ -417,7 +417,8 @@ def main() -> int:
     # reference semantics (src/benchmark.zig:35-92): one event pair per launch, mean/min/max
     fn = mod.get_function(sel.name.decode())
     ka = nc.pack_args(opts, sel, dq.ptr, dk.ptr, dv.ptr, do.ptr, module=mod)
-    per_launch = nc.run_kernel(fn, tuple(sel.grid), (sel.threads,), [ka], warmup=5, iters=args.ref_iters,
+    per_launch = nc.run_kernel(fn, tuple(sel.grid), (sel.threads,), nc.kernel_params(sel.name.decode(), ka),
+                               warmup=5, iters=args.ref_iters,
                                bytes_=work["bytes"], flops=work["flops_reference"], stream=stream.handle)
 
     # timed region: graphs of back-to-back launches

@@ -306,6 +306,19 @@ typedef struct nc_flash_kernel_args {
  * by-name launch writes nothing). */
 int nc_flash_kernel_scratch_bytes(const char *name, const nc_flash_options *opts, uint64_t *bytes);
 
+/* The kernel-parameter array (cuLaunchKernel style, for nc_function_launch and nc_benchmark_run_kernel)
+ * that launches the flash kernel `name` with the argument block `args`. Most kernels declare the block
+ * as one parameter: params[0] = args, *count = 1. The dense-layout kernels (`q1s8p1d`, `q1s8p2d`;
+ * packed slices: every slice
+ * stride seq_len*head_dim, every row stride head_dim; selected by nc_flash_select_kernel for such
+ * layouts) declare one parameter per field of the block, in order, so that their first seven are
+ * preloaded into SGPRs: params[i] = the address of field i, *count = NC_FLASH_MAX_KERNEL_PARAMS. Either
+ * way the kernarg segment is the block's bytes. `params` must hold `capacity` >= *count entries and
+ * stays valid while `args` does. NC_ERROR_NOT_FOUND for a name that is not a flash kernel. */
+#define NC_FLASH_MAX_KERNEL_PARAMS 20u
+int nc_flash_kernel_params(const char *name, nc_flash_kernel_args *args, void **params, uint32_t capacity,
+                           uint32_t *count);
+
 /* Fill the argument block for `sel` (row strides resolved, num_q_blocks derived). */
 int nc_flash_pack_args(const nc_flash_options *opts, const nc_flash_kernel_selection *sel,
                        const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o,

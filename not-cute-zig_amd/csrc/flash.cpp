@@ -44,6 +44,7 @@ struct Variant {
     Family family;
     bool bf16;  // the `_bf16` twin of the kernel (bf16 Q/K/V)
     bool xsplit = false;  // causal query blocks p and nqb-1-p shared by two workgroups (`x` kernels)
+    bool dense = false;   // dense-layout twin of a private-staging kernel (`d` kernels)
 
     uint32_t bm() const { return 32 * nq; }
     uint32_t bn() const { return 32 * ns * sub; }
@@ -68,6 +69,12 @@ struct Variant {
                                       C[0] == 'c', true, Family::kPipe, BF}
 // Pair split (flash_fwd.hip's XS kernels): d=64 causal, one query wave, eight key splits.
 #define PIPEX(D, T, BF) {"nc_flash_fwd_d" #D "_q1s8p2x_causal" T, D, 1, 8, 2, 1, true, true, Family::kPipe, BF, true}
+// Dense-layout private-staging kernels (flash_fwd.hip's `d` kernels: one parameter per field of the
+// argument block, slot from a 3-D workgroup id).
+#define PIPED(D, P, C, T, BF) {"nc_flash_fwd_d" #D "_q1s8p" #P "d_" C T, D, 1, 8, P, 1, C[0] == 'c', true, \
+                               Family::kPipe, BF, false, true}
+#define PIPED4(D, T, BF) PIPED(D, 2, "causal", T, BF), PIPED(D, 2, "full", T, BF), PIPED(D, 1, "causal", T, BF), \
+    PIPED(D, 1, "full", T, BF)
 // Two 32-key sub-tiles per wave per block ("t2": 32*NS*2 keys per block).
 #define PIPE2(D, NQ, NS, P, C, T, BF) {"nc_flash_fwd_d" #D "_q" #NQ "s" #NS "p" #P "t2_" C T, D, NQ, NS, P, 2, \
                                        C[0] == 'c', true, Family::kPipe, BF}
@@ -94,13 +101,16 @@ struct Variant {
     GEN(64, "full", false, "_unaligned", T, BF), GEN(64, "causal", false, "_unaligned", T, BF), PIPEX(64, T, BF), \
     GENG2(16, 1, 8, T, BF), GENG2(32, 1, 8, T, BF), GENG2(64, 1, 8, T, BF), GENG2(64, 4, 2, T, BF),          \
     PIPE(64, 1, 8, 1, "full", T, BF), PIPE(64, 1, 8, 1, "causal", T, BF), PIPE(32, 1, 8, 1, "full", T, BF),   \
-    PIPE(32, 1, 8, 1, "causal", T, BF), PIPE(16, 1, 8, 1, "full", T, BF), PIPE(16, 1, 8, 1, "causal", T, BF)
+    PIPE(32, 1, 8, 1, "causal", T, BF), PIPE(16, 1, 8, 1, "full", T, BF), PIPE(16, 1, 8, 1, "causal", T, BF), \
+    PIPED4(64, T, BF), PIPED4(32, T, BF), PIPED4(16, T, BF)
 
 const Variant kVariants[] = {VARIANTS("", false), VARIANTS("_bf16", true)};
 #undef VARIANTS
 #undef PIPE
 #undef PIPE2
 #undef PIPEX
+#undef PIPED
+#undef PIPED4
 #undef GEN
 #undef GENG
 #undef GENG2
@@ -108,7 +118,7 @@ const Variant kVariants[] = {VARIANTS("", false), VARIANTS("_bf16", true)};
 const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal, bool bf16) {
     for (const auto &v : kVariants)
         if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.causal == causal && v.bf16 == bf16 &&
-            !v.xsplit)
+            !v.xsplit && !v.dense)
             return &v;
     return nullptr;
 }
@@ -117,8 +127,27 @@ const Variant *find_pipe(uint32_t d, uint32_t nq, uint32_t ns, bool causal, bool
 const Variant *find_pipe_stages(uint32_t d, uint32_t nq, uint32_t ns, uint32_t nstage, bool causal, bool bf16) {
     for (const auto &v : kVariants)
         if (v.family == Family::kPipe && v.d == d && v.nq == nq && v.ns == ns && v.nstage == nstage &&
-            v.causal == causal && v.bf16 == bf16 && !v.xsplit)
+            v.causal == causal && v.bf16 == bf16 && !v.xsplit && !v.dense)
             return &v;
+    return nullptr;
+}
+
+// The dense-layout twin of a private-staging kernel, if there is one.
+const Variant *find_dense(const Variant &base) {
+    for (const auto &v : kVariants)
+        if (v.dense && v.d == base.d && v.nq == base.nq && v.ns == base.ns && v.nstage == base.nstage &&
+            v.causal == base.causal && v.bf16 == base.bf16)
+            return &v;
+    return nullptr;
+}
+
+// The table entry of a kernel name (a selection's name points into the table), or null.
+const Variant *variant_of(const char *name) {
+    if (!name) return nullptr;
+    for (const auto &v : kVariants)
+        if (v.name == name) return &v;
+    for (const auto &v : kVariants)
+        if (std::strcmp(v.name, name) == 0) return &v;
     return nullptr;
 }
 
@@ -364,6 +393,14 @@ const Variant *choose_pipe_layout(const nc_flash_options &o) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Every tensor a stack of packed slices: slice stride seq_len * d elements, row stride d.
+bool dense_layout(const nc_flash_options &o) {
+    const uint64_t d = o.head_dim, slice = o.seq_len * d;
+    return row_stride_of(o.q_row_stride, d) == d && row_stride_of(o.k_row_stride, d) == d &&
+           row_stride_of(o.v_row_stride, d) == d && row_stride_of(o.o_row_stride, d) == d && o.q_stride == slice &&
+           o.k_stride == slice && o.v_stride == slice && o.o_stride == slice;
+}
+
 int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selection *out) {
     if (!out) return NC_ERROR_INVALID_VALUE;
     int st = nc_flash_validate(opts);
@@ -401,14 +438,34 @@ int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selec
     const uint64_t nqb = (o.seq_len + v->bm() - 1) / v->bm();
     uint64_t grid = 0;
     if (mul_overflows(nqb, o.batch_heads, &grid) || grid > 0xffffffffull) return NC_ERROR_OVERFLOW;
+    uint32_t g3[3] = {(uint32_t)grid, 1u, 1u};
+    // Packed slices on a private-staging kernel: its dense-layout twin, whose waves reach their first
+    // loads without reading the argument block from memory. Measured on MI355X against the same
+    // kernel with the argument block (interleaved graph replays, bitwise-identical output): c3 5.71
+    // -> 5.49 us, BH=8 S=1536 causal 8.50 -> 8.16 us, BH=8 S=2048 causal 10.80 -> 10.52 us. Grid
+    // (8, BH/8, nqb) or (BH, 1, nqb): the same workgroups in the same linear order as the 1-D grid.
+    if (v->family == Family::kPipe && v->nq == 1 && !v->xsplit && dense_layout(o) && nqb <= 65535) {
+        const Variant *dv = find_dense(*v);
+        const uint64_t bh = o.batch_heads;
+        if (dv && (bh % 8 != 0 || bh / 8 <= 65535)) {
+            v = dv;
+            if (bh % 8 == 0) {
+                g3[0] = 8;
+                g3[1] = (uint32_t)(bh / 8);
+            } else {
+                g3[0] = (uint32_t)bh;
+            }
+            g3[2] = (uint32_t)nqb;
+        }
+    }
     std::memset(out, 0, sizeof *out);
     out->name = v->name;
     out->label = v->name;
     out->reference_name = reference_kernel(o);
     out->threads = v->threads();
-    out->grid[0] = (uint32_t)grid;
-    out->grid[1] = 1;
-    out->grid[2] = 1;
+    out->grid[0] = g3[0];
+    out->grid[1] = g3[1];
+    out->grid[2] = g3[2];
     out->block_m = v->bm();
     out->block_n = v->bn();
     out->kv_splits = v->ns;
@@ -545,7 +602,10 @@ int flash_launch_impl(nc_module module, const uint16_t *q, size_t q_len, const u
     cfg.block[2] = 1;
     cfg.shared_mem_bytes = 0;
     cfg.stream = stream;
-    void *params[] = {&args};
+    void *params[NC_FLASH_MAX_KERNEL_PARAMS];
+    uint32_t count = 0;
+    st = nc_flash_kernel_params(sel.name, &args, params, NC_FLASH_MAX_KERNEL_PARAMS, &count);
+    if (st) return st;
     return nc_function_launch(fn, &cfg, params);
 }
 
@@ -571,6 +631,28 @@ int nc_internal_flash_launch_scratch(nc_module module, const uint16_t *q, size_t
 int nc_flash_launch(nc_module module, const uint16_t *q, size_t q_len, const uint16_t *k, size_t k_len,
                     const uint16_t *v, size_t v_len, float *o, size_t o_len, const nc_flash_options *opts) {
     return nc_flash_launch_async(module, q, q_len, k, k_len, v, v_len, o, o_len, opts, nullptr);
+}
+
+int nc_flash_kernel_params(const char *name, nc_flash_kernel_args *args, void **params, uint32_t capacity,
+                           uint32_t *count) {
+    if (!name || !args || !params || !count) return NC_ERROR_INVALID_VALUE;
+    const Variant *v = variant_of(name);
+    if (!v) return NC_ERROR_NOT_FOUND;
+    if (!v->dense) {
+        if (capacity < 1) return NC_ERROR_INVALID_VALUE;
+        params[0] = args;
+        *count = 1;
+        return NC_SUCCESS;
+    }
+    void *fields[] = {&args->q, &args->k, &args->v, &args->o, &args->seq_len, &args->head_dim, &args->q_stride,
+                      &args->k_stride, &args->v_stride, &args->o_stride, &args->scale, &args->causal,
+                      &args->q_row_stride, &args->k_row_stride, &args->v_row_stride, &args->o_row_stride,
+                      &args->batch_heads, &args->num_q_blocks, &args->scratch, &args->balance_tail};
+    static_assert(sizeof fields / sizeof fields[0] == NC_FLASH_MAX_KERNEL_PARAMS, "one parameter per field");
+    if (capacity < NC_FLASH_MAX_KERNEL_PARAMS) return NC_ERROR_INVALID_VALUE;
+    for (uint32_t i = 0; i < NC_FLASH_MAX_KERNEL_PARAMS; ++i) params[i] = fields[i];
+    *count = NC_FLASH_MAX_KERNEL_PARAMS;
+    return NC_SUCCESS;
 }
 
 int nc_flash_kernel_scratch_bytes(const char *name, const nc_flash_options *opts, uint64_t *bytes) {

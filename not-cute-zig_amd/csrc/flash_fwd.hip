@@ -1400,6 +1400,42 @@ __device__ __forceinline__ void flash_fwd_pipe_kernel(const nc_flash_kernel_args
     flash_fwd_pipe_body<D, NQ, NS, CAUSAL, NSTAGE, SUB, BF, XS>(a, smem, [](uint32_t bh) { return pipe_slot(blockIdx.x, bh); });
 }
 
+// Dense-layout form of the private-staging kernels (the `d` kernels, e.g. q1s8p2d), for launches whose four
+// tensors are packed slices (slice stride seq_len*D elements, row stride D). The argument block is
+// the same nc_flash_kernel_args, declared as one kernel parameter per field so that the code object
+// asks for its first seven (q, k, v, o, seq_len, head_dim, q_stride: 14 SGPRs) to be preloaded into
+// SGPRs at wave launch; with the layout implied by seq_len and D, and the workgroup's slot taken
+// from its 3-D workgroup id, a wave reaches its first Q and K/V loads without waiting for any
+// memory. The other fields are read where they are needed (scale in the softmax, off the path to
+// the first loads). Grid (8, batch_heads/8, nqb) when batch_heads is a multiple of 8, else
+// (batch_heads, 1, nqb): workgroups are dealt to the XCDs in linear order, so with 8 in x each XCD
+// takes the heads x, x+8, ... (their K/V in its L2), and z runs from the heaviest causal block.
+template <int D, int NS, bool CAUSAL, int NSTAGE, bool BF>
+__device__ __forceinline__ void flash_fwd_dense_kernel(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o,
+                                                       uint64_t seq_len, uint64_t head_dim, float scale, void *scratch) {
+    __shared__ __attribute__((aligned(16))) char smem[pipe_lds_bytes<D, 1, NS, NSTAGE, 1, false>()];
+    nc_flash_kernel_args a;
+    const uint64_t slice = seq_len * D;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.seq_len = seq_len;
+    a.head_dim = head_dim;
+    a.q_stride = a.k_stride = a.v_stride = a.o_stride = slice;
+    a.scale = scale;
+    a.causal = CAUSAL ? 1u : 0u;
+    a.q_row_stride = a.k_row_stride = a.v_row_stride = a.o_row_stride = D;
+    a.batch_heads = 0;  // the slot comes from the workgroup id
+    a.num_q_blocks = (uint32_t)((seq_len + 31) / 32);
+    a.scratch = scratch;  // unused by these kernels but for the timeline code object's stamps
+    a.balance_tail = 0;
+    flash_fwd_pipe_body<D, 1, NS, CAUSAL, NSTAGE, 1, BF>(a, smem, [](uint32_t) {
+        const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);  // timeline stamps only
+        return PipeSlot{L, blockIdx.x + 8u * blockIdx.y, blockIdx.z};
+    });
+}
+
 // ---------------------------------------------------------------------------------------------
 // Reference-ABI entry points: the kernel symbols the reference's code object exports
 // (flash_attention_fwd_{v2,opt,h64,h64_bn32,h64_causal} and the legacy flash_attention_fwd,
@@ -2050,6 +2086,34 @@ NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p1_full, 32, 1, 8, false, 1, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d32_q1s8p1_causal, 32, 1, 8, true, 1, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p1_full, 16, 1, 8, false, 1, 1)
 NC_FLASH_PIPE_KERNEL(nc_flash_fwd_d16_q1s8p1_causal, 16, 1, 8, true, 1, 1)
+
+// Dense-layout private-staging kernels: nc_flash_kernel_args as one parameter per field (the first
+// seven preloaded into SGPRs; the Makefile builds this code object with
+// -amdgpu-kernarg-preload-count=7).
+#define NC_KARG_PARAMS                                                                                     \
+    const uint16_t *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t seq_len, uint64_t head_dim,  \
+        uint64_t q_stride, uint64_t k_stride, uint64_t v_stride, uint64_t o_stride, float scale, uint32_t causal, \
+        uint64_t q_row_stride, uint64_t k_row_stride, uint64_t v_row_stride, uint64_t o_row_stride,           \
+        uint32_t batch_heads, uint32_t num_q_blocks, void *scratch, uint32_t balance_tail
+#define NC_FLASH_DENSE_KERNEL(NAME, D, CAUSAL, NSTAGE)                                                       \
+    extern "C" __global__ __launch_bounds__(512) void NAME(NC_KARG_PARAMS) {                                 \
+        flash_fwd_dense_kernel<D, 8, CAUSAL, NSTAGE, false>(q, k, v, o, seq_len, head_dim, scale, scratch);   \
+    }                                                                                                       \
+    extern "C" __global__ __launch_bounds__(512) void NAME##_bf16(NC_KARG_PARAMS) {                          \
+        flash_fwd_dense_kernel<D, 8, CAUSAL, NSTAGE, true>(q, k, v, o, seq_len, head_dim, scale, scratch);    \
+    }
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d64_q1s8p2d_causal, 64, true, 2)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d64_q1s8p2d_full, 64, false, 2)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d64_q1s8p1d_causal, 64, true, 1)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d64_q1s8p1d_full, 64, false, 1)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d32_q1s8p2d_causal, 32, true, 2)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d32_q1s8p2d_full, 32, false, 2)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d32_q1s8p1d_causal, 32, true, 1)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d32_q1s8p1d_full, 32, false, 1)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d16_q1s8p2d_causal, 16, true, 2)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d16_q1s8p2d_full, 16, false, 2)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d16_q1s8p1d_causal, 16, true, 1)
+NC_FLASH_DENSE_KERNEL(nc_flash_fwd_d16_q1s8p1d_full, 16, false, 1)
 
 // Reference-ABI symbols (src/flash_v2.zig:23, src/flash_opt.zig:17, src/flash_h64.zig:21,
 // src/flash_h64_bn32.zig:26, src/flash_h64_causal.zig:20, src/kernels.zig:380): one body, launched

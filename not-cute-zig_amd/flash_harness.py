@@ -155,7 +155,8 @@ class Device:
         sel = nc.select_kernel(opts)
         fn = module.get_function(sel.name.decode())
         args = nc.pack_args(opts, sel, *[b.ptr for b in self.bufs], module=module)
-        return sel, nc.run_kernel(fn, tuple(sel.grid), (sel.threads,), [args], warmup=warmup, iters=iters,
+        return sel, nc.run_kernel(fn, tuple(sel.grid), (sel.threads,), nc.kernel_params(sel.name.decode(), args),
+                                  warmup=warmup, iters=iters,
                                   bytes_=bytes_, flops=flops)
 
     def free(self) -> None:
@@ -686,7 +687,8 @@ def cmd_timeline(args) -> int:
                 if label == "stamped":  # alternate buffers; bit 0 asks for the entry reading
                     a.scratch = stamp_bufs[i].ptr | (1 if args.anchor == "start" else 0)
                 blocks.append(a)
-            graph = nc.Graph.capture(stream, lambda: [fn.launch((grid,), (sel.threads,), [blocks[i % 2]],
+            params = [nc.kernel_params(name, blk) for blk in blocks]
+            graph = nc.Graph.capture(stream, lambda: [fn.launch(tuple(sel.grid), (sel.threads,), params[i % 2],
                                                                 stream=stream.handle) for i in range(args.launches)])
             for i in range(args.warmup):
                 graph.launch(stream)

@@ -229,6 +229,8 @@ _SIGS = {
     "nc_flash_select_kernel": (ctypes.c_int, [ctypes.POINTER(FlashOptions), ctypes.POINTER(KernelSelection)]),
     "nc_flash_select_kernel_for": (
         ctypes.c_int, [ctypes.POINTER(FlashOptions), _P, _P, _P, _P, ctypes.POINTER(KernelSelection)]),
+    "nc_flash_kernel_params": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_void_p, ctypes.POINTER(_P), ctypes.c_uint32,
+                                              ctypes.POINTER(ctypes.c_uint32)]),
     "nc_flash_pack_args": (
         ctypes.c_int,
         [ctypes.POINTER(FlashOptions), ctypes.POINTER(KernelSelection), _P, _P, _P, _P, ctypes.POINTER(KernelArgs)]),
@@ -363,6 +365,30 @@ def pack_args(opts: FlashOptions, sel: KernelSelection, q: int, k: int, v: int, 
             raise ValueError(f"{sel.name.decode()} needs {sel.scratch_bytes} bytes of scratch: pass the module")
         a.scratch = reserve_workspace(module, opts)
     return a
+
+
+MAX_KERNEL_PARAMS = 20  # NC_FLASH_MAX_KERNEL_PARAMS
+
+
+def kernel_params(name: str, args: KernelArgs) -> list:
+    """nc_flash_kernel_params as ctypes objects for Function.launch and run_kernel: [args] for a kernel
+    that takes the argument block as one parameter, else (the dense-layout `q1s8p1d`/`q1s8p2d` kernels) one
+    object per field,
+    each aliasing that field of `args`."""
+    arr = (_P * MAX_KERNEL_PARAMS)()
+    n = ctypes.c_uint32()
+    check(lib().nc_flash_kernel_params(name.encode(), ctypes.byref(args), arr, MAX_KERNEL_PARAMS, ctypes.byref(n)),
+          f"flash.kernelParams({name})")
+    if n.value == 1:
+        return [args]
+    base = ctypes.addressof(args)
+    views = []
+    for i, (fname, ftype) in enumerate(KernelArgs._fields_):
+        off = getattr(KernelArgs, fname).offset
+        if arr[i] != base + off:
+            raise RuntimeError(f"kernel_params({name}): parameter {i} is not field {fname}")
+        views.append(ftype.from_buffer(args, off))
+    return views
 
 
 def kernel_scratch_bytes(name: str, opts: FlashOptions) -> int:

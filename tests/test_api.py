@@ -166,7 +166,11 @@ def test_dispatch_geometry(d, causal, bh, s):
     name = sel.name.decode()
     assert f"_d{d}_" in name and name.endswith("_causal" if causal else "_full")
     assert sel.threads % 64 == 0 and 64 <= sel.threads <= 1024
-    assert sel.grid[0] == -(-s // sel.block_m) * bh and sel.grid[1] == sel.grid[2] == 1
+    nqb = -(-s // sel.block_m)
+    if re.search(r"_q1s8p\dd_", name):  # dense-layout twin: 3-D grid, the same workgroups in linear order
+        assert tuple(sel.grid) == ((8, bh // 8, nqb) if bh % 8 == 0 else (bh, 1, nqb))
+    else:
+        assert sel.grid[0] == nqb * bh and sel.grid[1] == sel.grid[2] == 1
     # 32 or 64 keys per key-split wave per staged block (one or two 32-key sub-tiles)
     assert sel.block_m % 32 == 0 and sel.block_n in (32 * sel.kv_splits, 64 * sel.kv_splits)
     assert sel.threads == 2 * sel.block_m * sel.kv_splits  # (block_m/32) query waves x splits x 64 lanes
@@ -175,7 +179,8 @@ def test_dispatch_geometry(d, causal, bh, s):
 
 
 def test_dispatch_headline_and_large_configs():
-    assert nc.select_kernel(CONFIGS["c3"].options()).name == b"nc_flash_fwd_d64_q1s8p2_causal"
+    c3 = nc.select_kernel(CONFIGS["c3"].options())
+    assert c3.name == b"nc_flash_fwd_d64_q1s8p2d_causal" and tuple(c3.grid) == (8, 1, 32)
     assert nc.select_kernel(CONFIGS["c4"].options()).name == b"nc_flash_fwd_d64_q8s1p2t2_full"
     assert nc.select_kernel(CONFIGS["c5"].options()).name == b"nc_flash_fwd_d64_q8s1p2t2_causal"
 
@@ -373,7 +378,7 @@ def test_dispatch_picks_measured_winner(case, kernel):
     d, bh, s, causal = case
     for dtype in ("f16", "bf16"):
         name = nc.select_kernel(nc.options(batch_heads=bh, seq_len=s, head_dim=d, causal=causal, dtype=dtype)).name
-        assert f"_{kernel}_" in name.decode(), (case, dtype, name)
+        assert re.search(rf"_{kernel}d?_", name.decode()), (case, dtype, name)  # d: its dense-layout twin
 
 
 @pytest.mark.parametrize("d,causal,s_last", [(64, True, 768), (64, False, 512), (32, True, 768), (32, False, 768),
@@ -384,7 +389,7 @@ def test_one_stage_private_kernel_boundary(d, causal, s_last):
     for dtype in ("f16", "bf16"):
         for s, stages in ((s_last, "p1"), (s_last + 1, "p2")):
             name = nc.select_kernel(nc.options(batch_heads=2, seq_len=s, head_dim=d, causal=causal, dtype=dtype)).name
-            assert f"_q1s8{stages}_" in name.decode(), (d, causal, s, dtype, name)
+            assert re.search(rf"_q1s8{stages}d?_", name.decode()), (d, causal, s, dtype, name)
 
 
 def test_pair_split_dispatch_region():
@@ -515,3 +520,47 @@ def test_noalloc_buffer_holds_every_dispatched_pair_split():
             sel = nc.select_kernel(Workload("x", bh, s, 64, True, 0.1, (("normal", 0, 1),) * 3).options())
             worst = max(worst, sel.scratch_bytes)
     assert 0 < worst <= cap, (worst, cap)
+
+
+def test_dense_twin_only_for_packed_slices():
+    """The private-staging kernels' dense-layout twins (q1s8p1d, q1s8p2d) take over exactly when every
+    tensor is a stack of packed slices (slice stride S*d, row stride d); any pad keeps the kernel that
+    reads the strides. Their 3-D grid holds the same workgroups: (8, BH/8, nqb) or (BH, 1, nqb)."""
+    def sel(**kw):
+        return nc.select_kernel(nc.options(**kw))
+
+    base = dict(batch_heads=8, seq_len=1024, head_dim=64, causal=True)
+    s = sel(**base)
+    assert s.name == b"nc_flash_fwd_d64_q1s8p2d_causal" and tuple(s.grid) == (8, 1, 32)
+    s = sel(**dict(base, batch_heads=3))
+    assert s.name == b"nc_flash_fwd_d64_q1s8p2d_causal" and tuple(s.grid) == (3, 1, 32)
+    s = sel(batch_heads=1, seq_len=32, head_dim=16)  # c1
+    assert s.name == b"nc_flash_fwd_d16_q1s8p1d_full" and tuple(s.grid) == (1, 1, 1)
+    # a padded slice of any one tensor, or padded rows, keep the strided kernel and a 1-D grid
+    for pad in (dict(q_stride=1024 * 64 + 8), dict(k_stride=1024 * 64 + 8), dict(v_stride=1024 * 64 + 8),
+                dict(o_stride=1024 * 64 + 4), dict(q_row_stride=72, q_stride=1024 * 72),
+                dict(o_row_stride=68, o_stride=1024 * 68)):
+        s = sel(**dict(base, **pad))
+        assert s.name == b"nc_flash_fwd_d64_q1s8p2_causal" and tuple(s.grid) == (256, 1, 1), pad
+    # c2's padded rows (pitch 40): the strided kernel
+    assert not re.search(r"q1s8p\dd_", nc.select_kernel(CONFIGS["c2_causal"].options()).name.decode())
+    # shared-staging selections have no dense twin
+    assert nc.select_kernel(CONFIGS["c4"].options()).name == b"nc_flash_fwd_d64_q8s1p2t2_full"
+
+
+def test_kernel_params_forms():
+    """nc_flash_kernel_params: the argument block as one parameter for most kernels, one parameter per
+    field (aliasing the block) for the dense-layout kernels; unknown names are refused."""
+    o = CONFIGS["c3"].options()
+    sel = nc.select_kernel(o)
+    a = nc.pack_args(o, sel, 0x1000, 0x2000, 0x3000, 0x4000)
+    p = nc.kernel_params(sel.name.decode(), a)
+    assert len(p) == nc.MAX_KERNEL_PARAMS == len(nc.KernelArgs._fields_)
+    assert [ctypes.addressof(x) for x in p] == [ctypes.addressof(a) + getattr(nc.KernelArgs, f).offset
+                                                 for f, _ in nc.KernelArgs._fields_]
+    assert p[0].value == 0x1000 and p[4].value == 1024 and p[6].value == 1024 * 64
+    for name in ("nc_flash_fwd_d64_q1s8p2_causal", "nc_flash_fwd_d64_q8s1p2t2_full", "nc_flash_fwd_d64_m64_causal"):
+        assert nc.kernel_params(name, a) == [a]
+    with pytest.raises(nc.NcError) as e:
+        nc.kernel_params("flash_attention_fwd_v2", a)
+    assert e.value.name == "NotFound"
