@@ -447,7 +447,7 @@ int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selec
     if (v->family == Family::kPipe && v->nq == 1 && !v->xsplit && dense_layout(o) && nqb <= 65535) {
         const Variant *dv = find_dense(*v);
         const uint64_t bh = o.batch_heads;
-        if (dv && (bh % 8 != 0 || bh / 8 <= 65535)) {
+        if (dv && (bh % 8 == 0 ? bh / 8 <= 65535 : bh <= 0x7fffffffu)) {  // grid y, z <= 65535; x < 2^31
             v = dv;
             if (bh % 8 == 0) {
                 g3[0] = 8;
