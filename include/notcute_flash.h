@@ -240,7 +240,10 @@ typedef struct nc_flash_kernel_selection {
     const char *label;          /* human-readable label */
     const char *reference_name; /* the kernel the reference's selectKernel picks for these options */
     uint32_t threads;           /* block size (multiple of 64: wave64) */
-    uint32_t grid[3];
+    uint32_t grid[3];           /* the launch grid (x, y, z) for `name` with these options; the kernels
+                                   derive each workgroup's slice and query block from its id and
+                                   do not re-check it, so a by-name launch with a larger grid
+                                   reads and writes outside the tensors */
     uint32_t block_m;           /* query rows per workgroup */
     uint32_t block_n;           /* keys staged per workgroup iteration */
     uint32_t kv_splits;         /* waves that share one query tile and split its keys */
