@@ -442,8 +442,8 @@ def test_kernel_scratch_bytes_refuses_more_pairs_than_counters():
     assert nc.kernel_scratch_bytes("nc_flash_fwd_d64_q1s8p2_causal", opts(64, 16448)) == 0
 
 
-# C struct name of each ctypes mirror. A foreign binding (the Zig `@cImport` of the header that
-# INTEGRATION.md sketches, ctypes here) maps its fields onto exactly these offsets and sizes.
+# C struct name of each ctypes mirror. A foreign binding (a Zig `@cImport` of the header, ctypes
+# here) maps its fields onto exactly these offsets and sizes.
 _ABI_STRUCTS = {
     "nc_flash_options": nc.FlashOptions,
     "nc_flash_kernel_selection": nc.KernelSelection,
@@ -489,8 +489,8 @@ def test_header_struct_layout_matches_binding(tmp_path):
 
 
 def test_options_fields_a_binding_sets():
-    """What a binding's toC (INTEGRATION.md's Zig sketch: nc_flash_options_init, then every field,
-    causal as @intFromBool) relies on: element_type defaults to f16, causal 1 selects the causal
+    """What a binding's toC (a Zig conversion of flash.Options: nc_flash_options_init, then every
+    field, causal as @intFromBool) relies on: element_type defaults to f16, causal 1 selects the causal
     kernel and 0 the non-causal one, bf16 selects the _bf16 twin."""
     o = nc.FlashOptions()
     nc.load_library().nc_flash_options_init(ctypes.byref(o))
