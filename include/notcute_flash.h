@@ -254,7 +254,9 @@ typedef struct nc_flash_kernel_selection {
 
 /* selectKernel (src/flash.zig:78-96), re-tuned for MI355X. Assumes 16-byte aligned base pointers
  * (what nc_malloc returns); nc_flash_launch re-checks the actual pointers. Calls nc_flash_validate
- * first and fails with its status. */
+ * first and fails with its status; NC_ERROR_OVERFLOW when the launch grid would exceed 2^32 - 1
+ * work-items in a dimension (about 2^23 workgroups of 512 threads: batch_heads * ceil(seq_len/32)
+ * at that size, where no packed-slice 3-D grid applies). */
 int nc_flash_select_kernel(const nc_flash_options *opts, nc_flash_kernel_selection *out);
 
 /* Same, for the actual buffers: picks the element-wise variant when a pointer or stride breaks

@@ -458,6 +458,8 @@ int select_impl(const nc_flash_options *opts, bool vec_ok, nc_flash_kernel_selec
             g3[2] = (uint32_t)nqb;
         }
     }
+    // The dispatch packet holds each grid dimension in work-items, as 32 bits.
+    if ((uint64_t)g3[0] * v->threads() > 0xffffffffull) return NC_ERROR_OVERFLOW;
     std::memset(out, 0, sizeof *out);
     out->name = v->name;
     out->label = v->name;

@@ -132,6 +132,26 @@ def test_validate_overflow():
     assert _status(o) == "Overflow"
 
 
+def test_select_grid_within_dispatch_limit():
+    """A dispatch packet holds each grid dimension in work-items as 32 bits: the selection refuses a
+    grid past 2^32 - 1 threads in x (2^24 one-block slices of workgroups of at least 256 threads) and
+    keeps every accepted grid within it."""
+    def sel(bh, **kw):
+        return nc.options(batch_heads=bh, seq_len=32, head_dim=16, **kw)
+
+    for kw in ({}, dict(q_stride=40 * 32, k_stride=40 * 32, v_stride=40 * 32, o_stride=40 * 32)):
+        with pytest.raises(nc.NcError) as e:
+            nc.select_kernel(sel(1 << 24, **kw))
+        assert e.value.name == "Overflow", kw
+        for bh in ((1 << 23) - 8, 1 << 23, (1 << 24) - 8):
+            try:
+                s = nc.select_kernel(sel(bh, **kw))
+            except nc.NcError as err:
+                assert err.name == "Overflow" and bh > 1 << 23, (bh, kw)
+                continue
+            assert s.grid[0] * s.threads <= 0xFFFFFFFF and s.grid[1] <= 65535 and s.grid[2] <= 65535, (bh, kw)
+
+
 # The reference's selectKernel decisions at every boundary of src/flash.zig:83-95, hand-tabulated.
 REFERENCE_DISPATCH = [
     # (d, S, BH, causal) -> reference kernel
